@@ -1,0 +1,353 @@
+"""Pins the CPU oracle (oracle/oracle.py) before anything is compared against it.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term,
+a wrong sign or index, a wrong rounding/summation order) fails one of them:
+golden vectors from the independent scalar C oracle, hand-derived known
+answers, closed forms and brute force on tiny inputs.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle as C
+from oracle import oracle as O
+
+GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+DIMS = (32, 64, 128, 256)
+
+
+# ---------------------------------------------------------------- golden vectors
+@pytest.mark.parametrize("d", DIMS)
+def test_encode_matches_golden(d):
+    x = GOLDEN[f"enc_d{d}_x"]
+    b = O.binary_encode(x)
+    assert np.array_equal(b.words, GOLDEN[f"enc_d{d}_words"])
+    assert np.array_equal(b.scale.view(np.uint16), GOLDEN[f"enc_d{d}_scale"])
+    r = O.residual_encode(x, b)
+    assert np.array_equal(r.codes, GOLDEN[f"enc_d{d}_codes"])
+    assert np.array_equal(r.scale.view(np.uint16), GOLDEN[f"enc_d{d}_rscale"])
+    _, ro = O.online_encode(x)
+    assert np.array_equal(ro.codes, GOLDEN[f"enc_d{d}_codes_online"])
+    assert np.array_equal(ro.scale.view(np.uint16), GOLDEN[f"enc_d{d}_rscale_online"])
+
+
+@pytest.mark.parametrize("d", DIMS)
+def test_scores_match_golden(d):
+    q = GOLDEN[f"qs_d{d}_q"]
+    k = GOLDEN[f"qs_d{d}_k"]
+    qw, sq, _ = O.query_prep(q)
+    assert np.array_equal(qw, GOLDEN[f"qs_d{d}_qwords"])
+    assert np.array_equal(sq.view(np.uint32), GOLDEN[f"qs_d{d}_scale_q"].view(np.uint32))
+    _, sqt, _ = O.query_prep_tree(q)
+    assert np.array_equal(sqt.view(np.uint32), GOLDEN[f"qs_d{d}_scale_q_tree"].view(np.uint32))
+    kb = O.binary_encode(k)
+    for i in range(q.shape[0]):
+        pc = O.popcounts(qw[i], kb.words)
+        assert np.array_equal(pc, GOLDEN[f"qs_d{d}_pc"][i])
+        xd = O.xnor_dot(sq[i], pc, kb.scale, d)
+        assert np.array_equal(xd.view(np.uint32), GOLDEN[f"qs_d{d}_xdot"][i].view(np.uint32))
+    ent = O.head_entropy(q[:, None, :].reshape(1, 3, d), O.BinaryEnc(
+        np.tile(kb.words, (3, 1)), np.tile(kb.scale, 3), np.tile(kb.mean32, 3)), 1, 3, 40)
+    np.testing.assert_allclose(ent[0], GOLDEN[f"qs_d{d}_entropy"], rtol=2e-6, atol=2e-6)
+
+
+# ---------------------------------------------------------------- known answers
+def test_sign_kats():
+    x = np.full((1, 32), 1.0, np.float16)
+    assert O.binary_encode(x).words[0, 0] == 0xFFFFFFFF
+    alt = np.where(np.arange(64) % 2 == 0, 1.0, -1.0).astype(np.float16)[None]
+    assert list(O.binary_encode(alt).words[0]) == [0x55555555, 0x55555555]
+    z = np.array([[0.0, -0.0] * 16], np.float16)
+    b = O.binary_encode(z)
+    assert b.words[0, 0] == 0xFFFFFFFF and float(b.scale[0]) == 0.0
+    nan = np.full((1, 32), np.nan, np.float16)
+    assert O.binary_encode(nan).words[0, 0] == 0
+
+
+def test_scale_closed_form():
+    # constant |x| = c: the mean is exactly c (sums of equal powers of two)
+    for d in DIMS:
+        for c in (0.5, 0.125, 3.0, 2.0 ** -10):
+            x = np.full((1, d), c, np.float16)
+            x[0, ::3] *= -1
+            assert float(O.binary_encode(x).scale[0]) == c
+
+
+def test_scale_tree_order_differs_from_sequential():
+    # choose values where the 128-thread tree order and a sequential sum round
+    # differently; the oracle must follow the tree (agreement with the C oracle
+    # which simulates the block literally).
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((4000, 128)) * 100).astype(np.float16)
+    b = O.binary_encode(x)
+    seq = np.zeros(4000, np.float32)
+    for i in range(128):
+        seq = (seq + np.abs(x[:, i].astype(np.float32))).astype(np.float32)
+    differs = (seq / np.float32(128)) != b.mean32
+    assert differs.any()          # the order is observable
+    w, s, m = C.binary_encode(x)
+    assert np.array_equal(m.view(np.uint32), b.mean32.view(np.uint32))
+
+
+def test_residual_kats():
+    # x = s + e with s the fp16 mean: residual codes at exact half-steps round half to even.
+    d = 32
+    # bits all 1, mean = 1.0 ; residuals r_i = x_i - 1
+    r = np.zeros(d, np.float32)
+    r[0] = 0.5       # absmax
+    r[1] = -0.5
+    r[2] = 0.5 / 14  # r*7/absmax = 0.5  -> 0 (half to even)
+    r[3] = 1.5 / 14  # 1.5 -> 2
+    r[4] = 2.5 / 14  # 2.5 -> 2
+    r[5:] = 0.0
+    # build x so that the mean stays 1.0: add compensating values pairwise
+    x = (1.0 + r).astype(np.float32)
+    x[6], x[7] = 1.0 - r[2], 1.0 - r[3]
+    x[8] = 1.0 - r[4]
+    x16 = x.astype(np.float16)[None]
+    b = O.binary_encode(x16)
+    s = float(b.scale[0])
+    rr = x16.astype(np.float32)[0] - s
+    enc = O.residual_encode(x16, b)
+    absmax = np.max(np.abs(rr))
+    exp = np.clip(np.rint(rr * np.float32(7.0 / absmax)), -7, 7)
+    assert np.array_equal(enc.codes[0], exp.astype(np.int8))
+    # absmax = 0 -> all codes 0 and scale 0
+    const = np.full((1, 64), 0.75, np.float16)
+    e = O.residual_encode(const, O.binary_encode(const))
+    assert (e.codes == 0).all() and float(e.scale[0]) == 0.0
+    # the element at absmax always maps to +-7
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((200, 128)).astype(np.float16)
+    b = O.binary_encode(x)
+    e = O.residual_encode(x, b)
+    assert (np.abs(e.codes).max(axis=1) == 7).all()
+
+
+def test_residual_reconstruction_bound():
+    rng = np.random.default_rng(2)
+    for d in DIMS:
+        x = (rng.standard_normal((300, d)) * 0.3).astype(np.float16)
+        b = O.binary_encode(x)
+        e = O.residual_encode(x, b)
+        rec = O.dequant_binary(b, d) + O.dequant_residual(e)
+        err = np.abs(rec - x.astype(np.float32))
+        # half a quantisation step plus the fp16 rounding of absmax (<= 2^-11 relative)
+        bound = e.scale.astype(np.float32)[:, None] * (1 / 14 + 2.0 ** -11) * 1.0001 + 1e-7
+        assert (err <= bound).all()
+
+
+def test_online_vs_two_step_differ_only_through_scale():
+    # B4: the online path uses the fp32 mean; when the mean is exactly
+    # representable in fp16 both paths are identical.
+    x = np.full((1, 128), 0.5, np.float16)
+    x[0, 5] = -0.5
+    b, r_on = O.online_encode(x)
+    r_two = O.residual_encode(x, b)
+    assert np.array_equal(r_on.codes, r_two.codes)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5000, 128)).astype(np.float16)
+    b, r_on = O.online_encode(x)
+    r_two = O.residual_encode(x, b)
+    diff = (r_on.codes != r_two.codes).any(axis=1)
+    exact = b.mean32 == b.scale.astype(np.float32)
+    assert not diff[exact].any()
+    assert diff.any()
+
+
+def test_nibble_pack_roundtrip_and_layout():
+    codes = np.arange(-7, 8, dtype=np.int8)
+    codes = np.concatenate([codes, codes[:1]])[None]          # 16 values
+    nib = O.pack_nibbles(codes)
+    assert nib[0, 0] == ((-7 & 0xF) | ((-6 & 0xF) << 4))
+    assert np.array_equal(O.unpack_nibbles(nib), codes)
+
+
+# ---------------------------------------------------------------- scores
+@pytest.mark.parametrize("d", DIMS)
+def test_popcount_closed_form(d):
+    rng = np.random.default_rng(d)
+    q = rng.standard_normal((4, d)).astype(np.float16)
+    k = rng.standard_normal((50, d)).astype(np.float16)
+    qw, sq, q32 = O.query_prep(q)
+    kb = O.binary_encode(k)
+    sgn_q = np.where(q.astype(np.float32) >= 0, 1, -1)
+    sgn_k = np.where(k.astype(np.float32) >= 0, 1, -1)
+    dots = sgn_q @ sgn_k.T
+    for i in range(4):
+        pc = O.popcounts(qw[i], kb.words)
+        assert np.array_equal(2 * pc - d, dots[i])
+    # q == k -> d ; q == -k -> -d
+    pc = O.popcounts(qw[0], O.binary_encode(q[:1]).words)
+    assert pc[0] == d
+    neg = (-q[:1].astype(np.float32)).astype(np.float16)
+    neg[neg == 0] = np.float16(-1.0)  # avoid +-0 which both map to bit 1
+    qq = q[:1].copy()
+    qq[qq == 0] = np.float16(1.0)
+    qwq, _, _ = O.query_prep(qq)
+    assert O.popcounts(qwq[0], O.binary_encode(neg).words)[0] == 0
+
+
+def test_scale_q_sequential_closed_form():
+    # powers of two with <= 24 significant bits in total: every partial sum is exact
+    q = np.array([[2.0 ** -i if i < 20 else 0.0 for i in range(32)]], np.float16)
+    _, sq, _ = O.query_prep(q)
+    exact = sum(2.0 ** -i for i in range(20))
+    assert float(sq[0]) == exact / 32
+
+
+def test_compensated_scores_closed_form():
+    """score = [(sq*sgn q).(sk*sgn k) + q.(n/7*rs)] / sqrt(d), evaluated in float64
+    by matmul over decoded K, must match the oracle's per-key restatement."""
+    rng = np.random.default_rng(7)
+    B, H, S, d = 1, 2, 64, 128
+    Q = (rng.standard_normal((B, H, d)) * 0.1).astype(np.float16)
+    K = (rng.standard_normal((B * H * S, d)) * 0.1).astype(np.float16)
+    V = (rng.standard_normal((B * H * S, d)) * 0.1).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    out, o32 = O.compensated_attention(Q, Kb, Kr, Vb, Vr, B, H, S, return_f32=True)
+    qw, sq, q32 = O.query_prep(Q.reshape(-1, d))
+    Kbin = O.dequant_binary(Kb, d).astype(np.float64).reshape(B * H, S, d)
+    Kres = O.dequant_residual(Kr).astype(np.float64).reshape(B * H, S, d)
+    Vrec = (O.dequant_binary(Vb, d) + O.dequant_residual(Vr)).astype(np.float64).reshape(B * H, S, d)
+    for i in range(B * H):
+        qb = sq[i] * np.where(q32[i] >= 0, 1.0, -1.0)
+        s = (Kbin[i] @ qb + Kres[i] @ q32[i].astype(np.float64)) / math.sqrt(d)
+        w = np.exp(s - s.max())
+        ref = (w @ Vrec[i]) / w.sum()
+        np.testing.assert_allclose(o32.reshape(B * H, d)[i], ref, rtol=1e-4, atol=1e-6)
+    # exact-order literal restatement agrees with the vectorised one
+    for i in range(B * H):
+        sl = slice(i * S, (i + 1) * S)
+        ex = O.compensated_attention_exact_order(
+            Q.reshape(-1, d)[i], O.BinaryEnc(Kb.words[sl], Kb.scale[sl], Kb.mean32[sl]),
+            O.ResidualEnc(Kr.codes[sl], Kr.scale[sl]), O.BinaryEnc(Vb.words[sl], Vb.scale[sl], Vb.mean32[sl]),
+            O.ResidualEnc(Vr.codes[sl], Vr.scale[sl]), S)
+        np.testing.assert_allclose(o32.reshape(B * H, d)[i], ex, rtol=2e-5, atol=2e-7)
+
+
+def test_attention_special_cases():
+    rng = np.random.default_rng(9)
+    d = 64
+    # S = 1 -> output is the V reconstruction
+    Q = rng.standard_normal((1, 1, d)).astype(np.float16)
+    K = rng.standard_normal((1, d)).astype(np.float16)
+    V = rng.standard_normal((1, d)).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    out, o32 = O.compensated_attention(Q, Kb, Kr, Vb, Vr, 1, 1, 1, return_f32=True)
+    vrec = O.dequant_binary(Vb, d) + O.dequant_residual(Vr)
+    np.testing.assert_allclose(o32[0, 0], vrec[0], rtol=1e-6)
+    # all keys identical -> equal weights -> mean of V reconstructions
+    S = 37
+    K = np.repeat(K, S, axis=0)
+    V = rng.standard_normal((S, d)).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    _, o32 = O.compensated_attention(Q, Kb, Kr, Vb, Vr, 1, 1, S, return_f32=True)
+    vrec = O.dequant_binary(Vb, d) + O.dequant_residual(Vr)
+    np.testing.assert_allclose(o32[0, 0], vrec.mean(axis=0), rtol=1e-5, atol=1e-7)
+    _, b32 = O.binary_attention(Q, Kb, Vb, 1, 1, S, return_f32=True)
+    np.testing.assert_allclose(b32[0, 0], O.dequant_binary(Vb, d).mean(axis=0), rtol=1e-5, atol=1e-7)
+
+
+def test_gqa_equals_mha_on_repeated_kv():
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, S, d = 2, 4, 2, 33, 64
+    Q = rng.standard_normal((B, Hq, d)).astype(np.float16)
+    K = rng.standard_normal((B, Hkv, S, d)).astype(np.float16)
+    V = rng.standard_normal((B, Hkv, S, d)).astype(np.float16)
+    Kb, Kr = O.encode_fused(K.reshape(-1, d))
+    Vb, Vr = O.encode_fused(V.reshape(-1, d))
+    gqa = O.compensated_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv)
+    Kx = np.repeat(K, Hq // Hkv, axis=1).reshape(-1, d)
+    Vx = np.repeat(V, Hq // Hkv, axis=1).reshape(-1, d)
+    Kb2, Kr2 = O.encode_fused(Kx)
+    Vb2, Vr2 = O.encode_fused(Vx)
+    mha = O.compensated_attention(Q, Kb2, Kr2, Vb2, Vr2, B, Hq, S)
+    assert np.array_equal(gqa.view(np.uint16), mha.view(np.uint16))
+
+
+def test_entropy_closed_form():
+    rng = np.random.default_rng(13)
+    B, H, S, d = 1, 3, 500, 128
+    Q = rng.standard_normal((B, H, d)).astype(np.float16)
+    K = rng.standard_normal((B * H * S, d)).astype(np.float16)
+    Kb = O.binary_encode(K)
+    ent = O.head_entropy(Q, Kb, B, H, S)
+    qw, sq, _ = O.query_prep_tree(Q.reshape(-1, d))
+    for h in range(H):
+        sl = slice(h * S, (h + 1) * S)
+        pc = O.popcounts(qw[h], Kb.words[sl])
+        s = (sq[h] * Kb.scale[sl].astype(np.float64)) * (2 * pc - d)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        H_ref = -(p * np.log(np.where(p > 0, p, 1))).sum()
+        assert abs(ent[0, h] - H_ref) < 1e-4 * max(1.0, abs(H_ref))
+
+
+def test_reference_attention_closed_form():
+    rng = np.random.default_rng(17)
+    B, H, S, d = 1, 2, 70, 64
+    Q = rng.standard_normal((B, H, d)).astype(np.float16)
+    K = rng.standard_normal((B, H, S, d)).astype(np.float16)
+    V = rng.standard_normal((B, H, S, d)).astype(np.float16)
+    _, o32 = O.reference_attention(Q, K, V, B, H, S, return_f32=True)
+    for h in range(H):
+        s = K[0, h].astype(np.float64) @ Q[0, h].astype(np.float64) / math.sqrt(d)
+        w = np.exp(s - s.max())
+        ref = w @ V[0, h].astype(np.float64) / w.sum()
+        np.testing.assert_allclose(o32[0, h], ref, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- top-k
+def test_topk_bruteforce_and_ties():
+    key = np.array([3, 1, 3, 2, 3, 0, -1, 3], np.float32)
+    assert list(O.topk_select(key, 3)) == [0, 2, 4]
+    assert list(O.topk_select(key, 5)) == [0, 2, 3, 4, 7]
+    rng = np.random.default_rng(19)
+    for _ in range(50):
+        S = int(rng.integers(1, 60))
+        key = rng.integers(-3, 4, S).astype(np.float32) * np.float32(0.5)
+        k = int(rng.integers(0, S + 1))
+        sel = O.topk_select(key, k)
+        # brute force: rank = number of keys strictly better (greater, or equal with lower index)
+        ranks = [sum(1 for j in range(S) if key[j] > key[i] or (key[j] == key[i] and j < i)) for i in range(S)]
+        assert set(sel) == {i for i in range(S) if ranks[i] < k}
+
+
+def test_topk_key_canonicalisation_and_exactness():
+    ks = np.array([0.0, 1.5, np.nan, 65504.0], np.float16)
+    pc = np.array([10, 64, 64, 0], np.int32)
+    key = O.topk_key(ks, pc, 128)
+    assert np.signbit(key[0]) == False  # -0 -> +0
+    assert key[2] == -np.inf
+    assert key[3] == np.float32(65504.0) * np.float32(-128)
+    assert O.default_top_k(131072) == 13108
+    assert O.default_top_k(30) == 3 and O.default_top_k(31) == 4
+
+
+def test_adaptive_all_selected_equals_compensated_and_none_equals_binary():
+    rng = np.random.default_rng(23)
+    B, Hq, Hkv, S, d = 1, 4, 2, 50, 128
+    Q = (rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)
+    K = (rng.standard_normal((B * Hkv * S, d)) * 0.3).astype(np.float16)
+    V = (rng.standard_normal((B * Hkv * S, d)) * 0.3).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    _, a32 = O.adaptive_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, S, n_kv_heads=Hkv, return_f32=True)
+    _, c32 = O.compensated_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    np.testing.assert_allclose(a32, c32, rtol=1e-6, atol=1e-7)
+    _, a0 = O.adaptive_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, 0, n_kv_heads=Hkv, return_f32=True)
+    _, b0 = O.binary_attention(Q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    np.testing.assert_allclose(a0, b0, rtol=1e-6, atol=1e-7)
+
+
+def test_ring_state():
+    r = O.RingState(3)
+    slots = [r.append() for _ in range(7)]
+    assert slots == [0, 1, 2, 0, 1, 2, 0]
+    assert r.filled == 3 and r.write_pos == 1
