@@ -1,0 +1,343 @@
+// Adaptive precision: exact top-k residual selection per (b, query head).
+//
+// The ranking key of key s is scale_k * (2*popcount - d) (exact in fp32),
+// mapped to an order-preserving uint32 u.  The k-th largest u is found by a
+// radix select over three digits (bits 31..21, 20..10, 9..0): each pass
+// histograms the digit of the keys that still match the prefix found so far
+// (LDS histograms flushed with atomics), and a one-block scan per (b, head)
+// picks the digit where the running count from the top reaches k.  After the
+// third pass the threshold T and the number `need` of keys equal to T that
+// are still to be taken are exact.  Ties at T are taken in key order: a
+// per-64-key-tile count of ties is prefix-summed, and the attention kernel
+// ranks ties inside a tile with a ballot.
+//
+// Workspace: hist [B*Hq][2048] u32 | state [B*Hq] (prefix u32, remaining i32)
+//            | ties [B*Hq][n_tiles] i32 | attention partials.
+#include "common.h"
+
+namespace bc {
+int run_attention(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                  const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
+                  int seq_len, int kv_stride, int head_dim, void* workspace,
+                  size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
+                  const int32_t* need, const int32_t* tie_prefix, uint8_t* selected);
+size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
+}  // namespace bc
+
+namespace {
+
+constexpr int kBins = 2048;
+
+struct SelArgs {
+    const uint16_t* q;
+    BinPlanes kb;
+    int Hq, Hkv, S, kv_stride, n_tiles;
+    uint32_t* hist;      // [B*Hq][2048]
+    uint32_t* prefix;    // [B*Hq]
+    int32_t* remain;     // [B*Hq]
+    int32_t* ties;       // [B*Hq][n_tiles]
+};
+
+template <int D, int G>
+__device__ void load_q_signs(const uint16_t* qb, uint32_t (*qs)[D / 32]) {
+    for (int i = threadIdx.x; i < G * (D / 32); i += blockDim.x) {
+        const int g = i / (D / 32), w = i % (D / 32);
+        uint32_t bits = 0;
+        for (int b = 0; b < 32; b++) bits |= (h2f(qb[g * D + 32 * w + b]) >= 0.0f ? 1u : 0u) << b;
+        qs[g][w] = bits;
+    }
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t key_of(const uint32_t* qs, const SignWords<D>& ks, float sk) {
+    int pc = 0;
+#pragma unroll
+    for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
+    return ordered_key(sk * (float)(2 * pc - D));
+}
+
+// Histogram of digit `pass` over keys matching prefix[bhq] in the higher digits.
+// grid: (splits, B*Hkv*(group/G)); block 256; each thread strides over keys.
+template <int D, int G>
+__global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chunk) {
+    __shared__ uint32_t qs[G][D / 32];
+    __shared__ uint32_t h[G][kBins];
+    const int nqg = (a.Hq / a.Hkv) / G;
+    const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
+    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+    const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
+    load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
+    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) (&h[0][0])[i] = 0u;
+    __syncthreads();
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
+    const int pbits = pass == 0 ? 0 : (pass == 1 ? 11 : 22);
+    uint32_t pref[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) pref[g] = pass == 0 ? 0u : a.prefix[bhq0 + g];
+    const int64_t base = (int64_t)bkv * a.kv_stride;
+    const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
+    for (int s = k0 + threadIdx.x; s < k1; s += blockDim.x) {
+        const SignWords<D> ks = load_signs<D>(a.kb.signs + (base + s) * (D / 8));
+        const float sk = h2f(a.kb.scales[base + s]);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint32_t u = key_of<D>(qs[g], ks, sk);
+            const bool match = pbits == 0 || (u >> (32 - pbits)) == (pref[g] >> (32 - pbits));
+            if (match) atomicAdd(&h[g][(u >> shift) & dmask], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) {
+        const uint32_t c = (&h[0][0])[i];
+        const int g = i / kBins, bin = i % kBins;
+        if (c) atomicAdd(&a.hist[(int64_t)(bhq0 + g) * kBins + bin], c);
+    }
+}
+
+// One block per (b, query head): pick the digit holding the remain-th largest
+// key, extend the prefix, and clear the histogram for the next pass.
+__global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_k) {
+    __shared__ uint32_t cnt[kBins];
+    __shared__ uint32_t part[256];
+    const int bhq = blockIdx.x;
+    uint32_t* h = a.hist + (int64_t)bhq * kBins;
+    const int nbins = pass == 2 ? 1024 : 2048;
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
+        cnt[i] = h[i];
+        h[i] = 0u;
+    }
+    __syncthreads();
+    int remain = pass == 0 ? top_k : a.remain[bhq];
+    uint32_t prefix = pass == 0 ? 0u : a.prefix[bhq];
+    // per-thread counts of 8 consecutive bins (descending digits)
+    const int per = kBins / 256;
+    uint32_t local = 0;
+    for (int j = 0; j < per; j++) {
+        const int d = nbins - 1 - (threadIdx.x * per + j);
+        if (d >= 0) local += cnt[d];
+    }
+    part[threadIdx.x] = local;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (remain <= 0) {
+            if (pass == 0) {
+                a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
+                a.remain[bhq] = 0;
+            }
+        } else {
+            uint32_t above = 0;
+            int t = 0;
+            for (; t < 256; t++) {
+                if (above + part[t] >= (uint32_t)remain) break;
+                above += part[t];
+            }
+            if (t == 256) {
+                // fewer matching keys than remain: select everything
+                a.prefix[bhq] = 0u;
+                a.remain[bhq] = 0;
+            } else {
+                int digit = 0;
+                for (int j = 0; j < per; j++) {
+                    const int d = nbins - 1 - (t * per + j);
+                    if (d < 0) break;
+                    if (above + cnt[d] >= (uint32_t)remain) {
+                        digit = d;
+                        break;
+                    }
+                    above += cnt[d];
+                }
+                a.prefix[bhq] = prefix | ((uint32_t)digit << shift);
+                a.remain[bhq] = remain - (int)above;
+            }
+        }
+    }
+}
+
+// Ties at the final threshold per 64-key tile.
+template <int D, int G>
+__global__ __launch_bounds__(256) void tie_count_kernel(SelArgs a, int chunk) {
+    __shared__ uint32_t qs[G][D / 32];
+    const int nqg = (a.Hq / a.Hkv) / G;
+    const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
+    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+    const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
+    load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
+    __syncthreads();
+    const int64_t base = (int64_t)bkv * a.kv_stride;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
+    for (int t0 = k0 + wave * 64; t0 < k1; t0 += 256) {
+        const int s = t0 + lane;
+        const bool valid = s < k1;
+        const int64_t vi = base + (valid ? s : t0);
+        const SignWords<D> ks = load_signs<D>(a.kb.signs + vi * (D / 8));
+        const float sk = h2f(a.kb.scales[vi]);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint32_t T = a.prefix[bhq0 + g];
+            const bool tie = valid && key_of<D>(qs[g], ks, sk) == T;
+            const uint64_t m = __ballot(tie);
+            if (lane == 0) a.ties[(int64_t)(bhq0 + g) * a.n_tiles + (t0 >> 6)] = __builtin_popcountll(m);
+        }
+    }
+}
+
+// Exclusive prefix over tiles, one block per (b, query head).
+__global__ __launch_bounds__(256) void tie_scan_kernel(int32_t* ties, int n_tiles) {
+    __shared__ int32_t part[256];
+    int32_t* t = ties + (int64_t)blockIdx.x * n_tiles;
+    const int per = (n_tiles + 255) / 256;
+    const int lo = threadIdx.x * per, hi = min(n_tiles, lo + per);
+    int32_t sum = 0;
+    for (int i = lo; i < hi; i++) sum += t[i];
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t run = 0;
+        for (int i = 0; i < 256; i++) {
+            const int32_t v = part[i];
+            part[i] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    int32_t run = part[threadIdx.x];
+    for (int i = lo; i < hi; i++) {
+        const int32_t v = t[i];
+        t[i] = run;
+        run += v;
+    }
+}
+
+__global__ void zero_kernel(uint32_t* p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+int pick_g(int group) {
+    if (group % 8 == 0) return 8;
+    if (group % 4 == 0) return 4;
+    if (group % 2 == 0) return 2;
+    return 1;
+}
+
+struct Layout {
+    size_t hist, prefix, remain, ties, attn, total;
+};
+
+Layout layout(int batch, int hq, int hkv, int S, int d) {
+    Layout L;
+    const size_t bh = (size_t)batch * hq;
+    const size_t n_tiles = (size_t)(S + 63) / 64;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    L.hist = 0;
+    L.prefix = al(L.hist + bh * kBins * 4);
+    L.remain = al(L.prefix + bh * 4);
+    L.ties = al(L.remain + bh * 4);
+    L.attn = al(L.ties + bh * (n_tiles ? n_tiles : 1) * 4);
+    L.total = L.attn + bc::attention_ws_bytes(batch, hq, hkv, S, d);
+    return L;
+}
+
+template <int D, int G>
+void run_passes(const SelArgs& a, int splits_y, int chunk, int nsplit, int bh, int top_k,
+                hipStream_t st) {
+    const dim3 grid(nsplit, splits_y);
+    for (int pass = 0; pass < 3; pass++) {
+        hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a, pass, chunk);
+        hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, pass, top_k);
+    }
+    hipLaunchKernelGGL((tie_count_kernel<D, G>), grid, dim3(256), 0, st, a, chunk);
+    hipLaunchKernelGGL(tie_scan_kernel, dim3(bh), dim3(256), 0, st, a.ties, a.n_tiles);
+}
+
+template <int D>
+void run_passes_g(int G, const SelArgs& a, int groups, int chunk, int nsplit, int bh, int top_k,
+                  hipStream_t st) {
+    switch (G) {
+        case 8: run_passes<D, 8>(a, groups, chunk, nsplit, bh, top_k, st); break;
+        case 4: run_passes<D, 4>(a, groups, chunk, nsplit, bh, top_k, st); break;
+        case 2: run_passes<D, 2>(a, groups, chunk, nsplit, bh, top_k, st); break;
+        default: run_passes<D, 1>(a, groups, chunk, nsplit, bh, top_k, st); break;
+    }
+}
+
+}  // namespace
+
+extern "C" int bc_adaptive_attention_workspace_size(int batch, int n_heads, int n_kv_heads,
+                                                    int seq_len, int head_dim, size_t* bytes) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED, "head_dim %d unsupported", head_dim);
+    BC_REQUIRE(batch >= 0 && n_heads >= 0 && n_kv_heads > 0 && seq_len >= 0 &&
+                   n_heads % n_kv_heads == 0,
+               BC_ERR_INVALID_ARGUMENT, "invalid dims");
+    BC_REQUIRE(bytes != nullptr, BC_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = layout(batch, n_heads, n_kv_heads, seq_len, head_dim).total;
+    return BC_OK;
+}
+
+extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const void* k_res,
+                                     const void* v_bin, const void* v_res, void* out,
+                                     uint8_t* selected, int batch, int n_heads, int n_kv_heads,
+                                     int seq_len, int kv_stride, int head_dim, int top_k,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED, "head_dim %d unsupported", head_dim);
+    BC_REQUIRE(batch >= 0 && n_heads >= 0 && n_kv_heads > 0 && seq_len >= 0 &&
+                   n_heads % n_kv_heads == 0 && kv_stride >= seq_len,
+               BC_ERR_INVALID_ARGUMENT, "invalid dims");
+    BC_REQUIRE(top_k >= 0, BC_ERR_INVALID_ARGUMENT, "top_k must be >= 0");
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin && k_res && v_bin && v_res && out, BC_ERR_INVALID_ARGUMENT,
+               "null pointer");
+    const Layout L = layout(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    BC_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, BC_ERR_WORKSPACE,
+               "workspace of %zu bytes required, got %zu", L.total, workspace_bytes);
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t* ws = (uint8_t*)workspace;
+    const int bh = batch * n_heads;
+    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
+    SelArgs a{};
+    a.q = (const uint16_t*)q;
+    a.kb = bin_planes(k_bin, cap, head_dim);
+    a.Hq = n_heads;
+    a.Hkv = n_kv_heads;
+    a.S = seq_len;
+    a.kv_stride = kv_stride;
+    a.n_tiles = (seq_len + 63) / 64;
+    a.hist = (uint32_t*)(ws + L.hist);
+    a.prefix = (uint32_t*)(ws + L.prefix);
+    a.remain = (int32_t*)(ws + L.remain);
+    a.ties = (int32_t*)(ws + L.ties);
+    // clear the histograms with a kernel (no memset nodes: graph-capture safe)
+    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, a.hist, (int64_t)bh * kBins);
+    int rc = bc::check_launch("adaptive zero");
+    if (rc != BC_OK) return rc;
+    const int G = pick_g(n_heads / n_kv_heads);
+    const int groups = batch * n_kv_heads * ((n_heads / n_kv_heads) / G);
+    const int tiles = a.n_tiles;
+    int nsplit = (4 * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
+    if (nsplit > tiles) nsplit = tiles;
+    if (nsplit < 1) nsplit = 1;
+    const int tiles_per = (tiles + nsplit - 1) / nsplit > 0 ? (tiles + nsplit - 1) / nsplit : 1;
+    const int chunk = tiles_per * 64;
+    nsplit = (tiles + tiles_per - 1) / tiles_per;
+    if (nsplit < 1) nsplit = 1;
+    const int k = top_k > seq_len ? seq_len : top_k;
+    switch (head_dim) {
+        case 32: run_passes_g<32>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 64: run_passes_g<64>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 96: run_passes_g<96>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 128: run_passes_g<128>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 160: run_passes_g<160>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 192: run_passes_g<192>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 224: run_passes_g<224>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 256: run_passes_g<256>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
+    }
+    rc = bc::check_launch("adaptive select");
+    if (rc != BC_OK) return rc;
+    return bc::run_attention(2, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
+                             seq_len, kv_stride, head_dim, ws + L.attn, workspace_bytes - L.attn,
+                             st, a.prefix, a.remain, a.ties, selected);
+}

@@ -1,0 +1,965 @@
+// Split-KV decode attention over the compressed cache (binary, compensated and
+// adaptive top-k), per-key binary scores, head entropy, the exact fp16
+// attention baseline and the split combine.
+//
+// Work decomposition (one launch): grid.x = key split, grid.y = (b, kv head,
+// query-head group).  A 256-thread workgroup (4 wave64) owns one contiguous key
+// range of one kv head and G query heads that read that kv head (GQA: every
+// key tile is fetched once for all G heads).  Waves take 64-key tiles
+// round-robin.  Per tile:
+//   score phase  lane = key.  Popcount of the 64-bit sign words against the
+//                query's signs, the INT4 residual dot via v_dot2_f32_f16 on
+//                nibbles turned into fp16 pairs (see residual_dot_pairs), online
+//                softmax in the log2 domain with a wave max per tile.
+//   value phase  lane = (32-dim slice c, key subgroup r).  Each lane decodes
+//                the sign word and 4 dwords of codes of its keys and
+//                accumulates w*sv*sign + w*(rs/7)*n in fp32 registers.
+// The workgroup folds its 4 waves into one (m, l, acc[D]) partial per query
+// head in the workspace; attn_combine_kernel merges the splits.
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum AttnMode : int { MODE_BINARY = 0, MODE_COMP = 1, MODE_ADAPTIVE = 2 };
+
+struct AttnArgs {
+    const uint16_t* q;  // [B, Hq, D] fp16
+    BinPlanes kb, vb;
+    ResPlanes kr, vr;
+    int B, Hq, Hkv, S, kv_stride;
+    int n_splits, chunk;  // chunk: keys per split (multiple of 64)
+    float* ws;            // [B*Hq][n_splits][D + 2]: m (log2 domain), l, acc[D]
+    // adaptive selection (MODE_ADAPTIVE)
+    const uint32_t* thresh;      // [B*Hq] ordered key threshold
+    const int32_t* need;         // [B*Hq] ties at the threshold still to take
+    const int32_t* tie_prefix;   // [B*Hq][n_tiles] ties in earlier 64-key tiles
+    int n_tiles;
+    uint8_t* selected;           // optional [B, Hq, S]
+};
+
+template <int D>
+struct QPrep {
+    // per query head, in LDS
+    uint32_t signs[D / 32];
+    uint32_t pairs[D / 8][4];  // fp16 pairs (q[8w+t], q[8w+4+t]) for the nibble dot
+    float scale_q;             // sequential mean |q| (src/compensated_attention.cu:65-67)
+    float offset;              // 1032 * sum(q): removed from the magic-number dot
+};
+
+// Residual dot sum_i q_i * n_i for one key whose codes are D/8 dwords.
+// Each dword holds 8 nibbles (element 8w+t in bits 4t..4t+3).  XOR 0x8 turns
+// a two's-complement nibble n into u = n + 8 in [0, 15]; OR-ing u into the
+// mantissa of fp16 1024.0 (0x6400) gives the exact fp16 value 1024 + u, two
+// elements per dword, so v_dot2_f32_f16 accumulates q*(1032 + n).  The
+// constant 1032*sum(q) is subtracted once per key.
+template <int D>
+__device__ __forceinline__ float residual_dot_pairs(const uint32_t* codes, const QPrep<D>& qp) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < D / 8; w++) {
+        const uint32_t x = codes[w] ^ 0x88888888u;
+        const uint4 qv = *(const uint4*)qp.pairs[w];
+        const uint32_t p0 = (x & 0x000F000Fu) | 0x64006400u;
+        const uint32_t p1 = ((x >> 4) & 0x000F000Fu) | 0x64006400u;
+        const uint32_t p2 = ((x >> 8) & 0x000F000Fu) | 0x64006400u;
+        const uint32_t p3 = ((x >> 12) & 0x000F000Fu) | 0x64006400u;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qv.x), __builtin_bit_cast(h2, p0), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qv.y), __builtin_bit_cast(h2, p1), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qv.z), __builtin_bit_cast(h2, p2), acc, false);
+        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qv.w), __builtin_bit_cast(h2, p3), acc, false);
+    }
+    return acc - qp.offset;
+}
+
+// Fill QPrep for G query heads from global Q (all 256 threads participate).
+template <int D, int G>
+__device__ void prep_queries(const uint16_t* qbase, QPrep<D>* qp, float* qf_scratch) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < G * D; i += blockDim.x) qf_scratch[i] = h2f(qbase[i]);
+    __syncthreads();
+    for (int i = tid; i < G * (D / 32); i += blockDim.x) {
+        const int g = i / (D / 32), w = i % (D / 32);
+        uint32_t bits = 0;
+        for (int b = 0; b < 32; b++) bits |= (qf_scratch[g * D + 32 * w + b] >= 0.0f ? 1u : 0u) << b;
+        qp[g].signs[w] = bits;
+    }
+    for (int i = tid; i < G * (D / 8) * 4; i += blockDim.x) {
+        const int g = i / (D / 2), r = i % (D / 2), w = r / 4, t = r % 4;
+        const uint32_t lo = qbase[g * D + 8 * w + t];
+        const uint32_t hi = qbase[g * D + 8 * w + 4 + t];
+        qp[g].pairs[w][t] = lo | (hi << 16);
+    }
+    if (tid < G) {
+        float acc = 0.0f, sum = 0.0f;
+        for (int i = 0; i < D; i++) {
+            acc += fabsf(qf_scratch[tid * D + i]);
+            sum += qf_scratch[tid * D + i];
+        }
+        qp[tid].scale_q = acc / (float)D;
+        qp[tid].offset = 1032.0f * sum;
+    }
+    __syncthreads();
+}
+
+template <int D, int G, int MODE>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+    constexpr int NW = D / 32;            // sign words per key
+    constexpr int LPK = D / 32;           // value-phase lanes per key (32 dims each)
+    constexpr int R = 64 / LPK;           // key subgroups in the value phase
+    constexpr int KPL = (64 + R - 1) / R; // keys per value lane per tile
+    constexpr bool RES = MODE != MODE_BINARY;
+
+    __shared__ QPrep<D> qp[G];
+    __shared__ float qf[G * D];
+    __shared__ float2 wl[4][G][64];       // per wave: (2*w*sv, w*rs/7) of each key
+    __shared__ uint32_t sel_lds[4][64];   // adaptive: per key bitmask over g
+    __shared__ float red[4][64][33];      // value-lane partials (padded)
+    __shared__ float wsum[4][G][D];
+    __shared__ float wm[4][G], wlsum[4][G];
+
+    const int split = blockIdx.x;
+    const int nqg = (a.Hq / a.Hkv) / G;
+    const int y = blockIdx.y;
+    const int qg = y % nqg;
+    const int bkv = y / nqg;  // b * Hkv + kvh
+    const int b = bkv / a.Hkv;
+    const int kvh = bkv % a.Hkv;
+    const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
+    const int bhq0 = b * a.Hq + hq0;
+
+    prep_queries<D, G>(a.q + (int64_t)bhq0 * D, qp, qf);
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int key_begin = split * a.chunk;
+    const int key_end = min(a.S, key_begin + a.chunk);
+    const int64_t kv_base = (int64_t)bkv * a.kv_stride;
+    const float isd2 = (1.0f / sqrtf((float)D)) * kLog2e;
+
+    // value-lane coordinates
+    const int vc = lane % LPK;
+    const int vr = lane / LPK;
+
+    float m[G], lsum[G], off[G];
+    float acc[G][32];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        lsum[g] = 0.0f;
+        off[g] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k++) acc[g][k] = 0.0f;
+    }
+
+    uint32_t thresh[G];
+    int need[G];
+    if constexpr (MODE == MODE_ADAPTIVE) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            thresh[g] = a.thresh[bhq0 + g];
+            need[g] = a.need[bhq0 + g];
+        }
+    }
+
+    for (int t0 = key_begin + wave * 64; t0 < key_end; t0 += 4 * 64) {
+        // ---------------- issue value loads (independent of scores)
+        uint4 vcodes[KPL];
+        uint32_t vsigns[KPL];
+#pragma unroll
+        for (int k = 0; k < KPL; k++) {
+            const int sl = vr + R * k;
+            const int s = t0 + sl;
+            vcodes[k] = make_uint4(0, 0, 0, 0);
+            vsigns[k] = 0;
+            if (vr < R && sl < 64 && s < key_end) {
+                const int64_t vi = kv_base + s;
+                vsigns[k] = ((const uint32_t*)(a.vb.signs + vi * (D / 8)))[vc];
+                if constexpr (MODE == MODE_COMP)
+                    vcodes[k] = ((const uint4*)(a.vr.codes + vi * (D / 2)))[vc];
+            }
+        }
+
+        // ---------------- score phase: lane = key
+        const int s = t0 + lane;
+        const bool valid = s < key_end;
+        const int64_t ki = kv_base + (valid ? s : t0);
+        const SignWords<D> ks = load_signs<D>(a.kb.signs + ki * (D / 8));
+        const float sk = h2f(a.kb.scales[ki]);
+        const float svv = h2f(a.vb.scales[ki]);
+        float rsk = 0.0f, rsv = 0.0f;
+        uint32_t kcodes[D / 8];
+        if constexpr (MODE == MODE_COMP) {
+            rsk = h2f(a.kr.scales[ki]);
+            rsv = h2f(a.vr.scales[ki]);
+            const uint4* cp = (const uint4*)(a.kr.codes + ki * (D / 2));
+#pragma unroll
+            for (int i = 0; i < D / 32; i++) {
+                const uint4 c = cp[i];
+                kcodes[4 * i] = c.x; kcodes[4 * i + 1] = c.y; kcodes[4 * i + 2] = c.z; kcodes[4 * i + 3] = c.w;
+            }
+        }
+
+        float sc[G];
+        uint32_t selmask = 0;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            int pc = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) pc += __builtin_popcount(~(qp[g].signs[w] ^ ks.w[w]));
+            const float mq = (float)(2 * pc - D);
+            // (scale_q * scale_k) * (2pc - d)   (src/xnor_dot.cuh:179)
+            const float xdot = (qp[g].scale_q * sk) * mq;
+            if constexpr (MODE == MODE_ADAPTIVE) {
+                const uint32_t key = ordered_key(sk * mq);
+                const uint64_t tie = __ballot(valid && key == thresh[g]);
+                bool sel = key > thresh[g];
+                if (key == thresh[g] && need[g] > 0) {
+                    // rank of this tie among all ties of the key range, in key order
+                    const int before = __builtin_popcountll(tie & ((1ull << lane) - 1ull));
+                    const int tile = t0 >> 6;
+                    sel = (a.tie_prefix[(int64_t)(bhq0 + g) * a.n_tiles + tile] + before) < need[g];
+                }
+                selmask |= (sel && valid) ? (1u << g) : 0u;
+            }
+            sc[g] = xdot;
+        }
+
+        if constexpr (MODE == MODE_ADAPTIVE) {
+            if (selmask) {
+                rsk = h2f(a.kr.scales[ki]);
+                rsv = h2f(a.vr.scales[ki]);
+                const uint4* cp = (const uint4*)(a.kr.codes + ki * (D / 2));
+#pragma unroll
+                for (int i = 0; i < D / 32; i++) {
+                    const uint4 c = cp[i];
+                    kcodes[4 * i] = c.x; kcodes[4 * i + 1] = c.y; kcodes[4 * i + 2] = c.z; kcodes[4 * i + 3] = c.w;
+                }
+            }
+            sel_lds[wave][lane] = selmask;
+            if (a.selected != nullptr && valid) {
+#pragma unroll
+                for (int g = 0; g < G; g++)
+                    a.selected[(int64_t)(bhq0 + g) * a.S + s] = (selmask >> g) & 1u;
+            }
+        }
+
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float score = sc[g];
+            if constexpr (MODE == MODE_COMP) {
+                const float rdot = residual_dot_pairs<D>(kcodes, qp[g]) * (rsk / 7.0f);
+                score = score + rdot;
+            } else if constexpr (MODE == MODE_ADAPTIVE) {
+                if ((selmask >> g) & 1u) {
+                    const float rdot = residual_dot_pairs<D>(kcodes, qp[g]) * (rsk / 7.0f);
+                    score = score + rdot;
+                }
+            }
+            float s2 = valid ? score * isd2 : -INFINITY;
+            const float mt = wave_max(s2);
+            const float mn = fmaxf(m[g], mt);
+            if (mn > m[g]) {
+                const float alpha = exp2f(m[g] - mn);
+                lsum[g] *= alpha;
+                off[g] *= alpha;
+#pragma unroll
+                for (int k = 0; k < 32; k++) acc[g][k] *= alpha;
+                m[g] = mn;
+            }
+            const float p = valid ? exp2f(s2 - mn) : 0.0f;
+            lsum[g] += p;
+            float rv = 0.0f;
+            if constexpr (MODE == MODE_COMP) rv = p * (rsv / 7.0f);
+            if constexpr (MODE == MODE_ADAPTIVE) rv = ((selmask >> g) & 1u) ? p * (rsv / 7.0f) : 0.0f;
+            wl[wave][g][lane] = make_float2(2.0f * p * svv, rv);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+
+        // ---------------- value phase: lane = (slice vc, subgroup vr)
+#pragma unroll
+        for (int k = 0; k < KPL; k++) {
+            const int sl = vr + R * k;
+            const int sv_ = t0 + sl;
+            if (!(vr < R && sl < 64 && sv_ < key_end)) continue;
+            uint4 codes = vcodes[k];
+            if constexpr (MODE == MODE_ADAPTIVE) {
+                if (sel_lds[wave][sl] != 0u) {
+                    const int64_t vi = kv_base + sv_;
+                    codes = ((const uint4*)(a.vr.codes + vi * (D / 2)))[vc];
+                }
+            }
+            const uint32_t sb = vsigns[k];
+            float fb[32];
+#pragma unroll
+            for (int e = 0; e < 32; e++) fb[e] = (float)((sb >> e) & 1u);
+            float fu[32];
+            if constexpr (RES) {
+                const uint32_t cw[4] = {codes.x, codes.y, codes.z, codes.w};
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t x = cw[w] ^ 0x88888888u;
+                    const uint32_t lo = x & 0x0F0F0F0Fu;
+                    const uint32_t hi = (x >> 4) & 0x0F0F0F0Fu;
+                    fu[8 * w + 0] = (float)((lo >> 0) & 0xFFu);
+                    fu[8 * w + 2] = (float)((lo >> 8) & 0xFFu);
+                    fu[8 * w + 4] = (float)((lo >> 16) & 0xFFu);
+                    fu[8 * w + 6] = (float)((lo >> 24) & 0xFFu);
+                    fu[8 * w + 1] = (float)((hi >> 0) & 0xFFu);
+                    fu[8 * w + 3] = (float)((hi >> 8) & 0xFFu);
+                    fu[8 * w + 5] = (float)((hi >> 16) & 0xFFu);
+                    fu[8 * w + 7] = (float)((hi >> 24) & 0xFFu);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float2 wv = wl[wave][g][sl];
+                // acc += 2*w*sv*bit - w*sv  +  w*rs/7*u - 8*w*rs/7
+                off[g] += 0.5f * wv.x;
+#pragma unroll
+                for (int e = 0; e < 32; e++) acc[g][e] = fmaf(wv.x, fb[e], acc[g][e]);
+                if constexpr (RES) {
+                    off[g] += 8.0f * wv.y;
+#pragma unroll
+                    for (int e = 0; e < 32; e++) acc[g][e] = fmaf(wv.y, fu[e], acc[g][e]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---------------- fold the workgroup into one partial per query head
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float l_w = wave_sum(lsum[g]);
+        if (lane == 0) {
+            wm[wave][g] = m[g];
+            wlsum[wave][g] = l_w;
+        }
+#pragma unroll
+        for (int e = 0; e < 32; e++) red[wave][lane][e] = acc[g][e] - off[g];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // lane j sums over subgroups for dims j, j + 64, ...
+        for (int i = lane; i < D; i += 64) {
+            const int c = i / 32, e = i % 32;
+            float sum = 0.0f;
+            for (int r = 0; r < R; r++) sum += red[wave][r * LPK + c][e];
+            wsum[wave][g][i] = sum;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+        const int g = i / D, d = i % D;
+        float M = -INFINITY;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+        float accv = 0.0f, lv = 0.0f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < 4; w++) {
+                const float f = (wm[w][g] == -INFINITY) ? 0.0f : exp2f(wm[w][g] - M);
+                accv += f * wsum[w][g][d];
+                lv += f * wlsum[w][g];
+            }
+        }
+        float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
+        dst[2 + d] = accv;
+        if (d == 0) {
+            dst[0] = M;
+            dst[1] = lv;
+        }
+    }
+}
+
+// Merge split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// Same normalisation as the reference (acc * (l > 0 ? 1/l : 0), fp16 store,
+// src/compensated_attention.cu:104-108).
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* ws, uint16_t* out,
+                                                           int n_splits) {
+    const int bh = blockIdx.x;
+    const float* p = ws + (int64_t)bh * n_splits * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; s++) M = fmaxf(M, p[s * (D + 2)]);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float accv = 0.0f, l = 0.0f;
+        if (M != -INFINITY) {
+            for (int s = 0; s < n_splits; s++) {
+                const float ms = p[s * (D + 2)];
+                const float f = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+                accv += f * p[s * (D + 2) + 2 + d];
+                l += f * p[s * (D + 2) + 1];
+            }
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        out[(int64_t)bh * D + d] = f2h(accv * inv);
+    }
+}
+
+// ---------------------------------------------------------------- fp16 reference
+// Exact attention over dense fp16 K/V [B, Hkv, S, D] with fp32 accumulation.
+// Same split/online-softmax structure; q.k via v_dot2_f32_f16 on fp16 pairs,
+// p*v via mixed-precision FMA.
+template <int D, int G>
+__global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const uint16_t* K,
+                                                       const uint16_t* V, int Hq, int Hkv, int S,
+                                                       int n_splits, int chunk, float* ws) {
+    constexpr int LPK = D / 8;   // value lanes per key: 8 dims (one uint4) each
+    constexpr int R = 64 / LPK;
+    constexpr int KPL = (64 + R - 1) / R;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    __shared__ uint32_t qpair[G][D / 2];
+    __shared__ float wl[4][G][64];
+    __shared__ float red[4][64][9];
+    __shared__ float wsum[4][G][D];
+    __shared__ float wm[4][G], wlsum[4][G];
+
+    const int split = blockIdx.x;
+    const int nqg = (Hq / Hkv) / G;
+    const int qg = blockIdx.y % nqg;
+    const int bkv = blockIdx.y / nqg;
+    const int b = bkv / Hkv, kvh = bkv % Hkv;
+    const int hq0 = kvh * (Hq / Hkv) + qg * G;
+    const int bhq0 = b * Hq + hq0;
+    for (int i = threadIdx.x; i < G * D / 2; i += blockDim.x)
+        qpair[i / (D / 2)][i % (D / 2)] = ((const uint32_t*)(q + (int64_t)bhq0 * D))[i];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int key_begin = split * chunk, key_end = min(S, key_begin + chunk);
+    const int64_t base = (int64_t)bkv * S;
+    const float isd2 = (1.0f / sqrtf((float)D)) * kLog2e;
+    const int vc = lane % LPK, vr = lane / LPK;
+    float m[G], lsum[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        lsum[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
+    }
+    for (int t0 = key_begin + wave * 64; t0 < key_end; t0 += 256) {
+        uint4 vv[KPL];
+#pragma unroll
+        for (int k = 0; k < KPL; k++) {
+            const int sl = vr + R * k, s = t0 + sl;
+            vv[k] = make_uint4(0, 0, 0, 0);
+            if (vr < R && sl < 64 && s < key_end) vv[k] = ((const uint4*)(V + (base + s) * D))[vc];
+        }
+        const int s = t0 + lane;
+        const bool valid = s < key_end;
+        const uint4* kp = (const uint4*)(K + (base + (valid ? s : t0)) * D);
+        float dots[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) dots[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D / 8; i++) {
+            const uint4 kk = kp[i];
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 0]), __builtin_bit_cast(h2, kk.x), dots[g], false);
+                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 1]), __builtin_bit_cast(h2, kk.y), dots[g], false);
+                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 2]), __builtin_bit_cast(h2, kk.z), dots[g], false);
+                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 3]), __builtin_bit_cast(h2, kk.w), dots[g], false);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float s2 = valid ? dots[g] * isd2 : -INFINITY;
+            const float mn = fmaxf(m[g], wave_max(s2));
+            if (mn > m[g]) {
+                const float alpha = exp2f(m[g] - mn);
+                lsum[g] *= alpha;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g][e] *= alpha;
+                m[g] = mn;
+            }
+            const float p = valid ? exp2f(s2 - mn) : 0.0f;
+            lsum[g] += p;
+            wl[wave][g][lane] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int k = 0; k < KPL; k++) {
+            const int sl = vr + R * k;
+            if (!(vr < R && sl < 64 && t0 + sl < key_end)) continue;
+            const uint32_t vw[4] = {vv[k].x, vv[k].y, vv[k].z, vv[k].w};
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = wl[wave][g][sl];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const h2 hv = __builtin_bit_cast(h2, vw[e]);
+                    acc[g][2 * e] = fmaf(p, (float)hv.x, acc[g][2 * e]);
+                    acc[g][2 * e + 1] = fmaf(p, (float)hv.y, acc[g][2 * e + 1]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float l_w = wave_sum(lsum[g]);
+        if (lane == 0) {
+            wm[wave][g] = m[g];
+            wlsum[wave][g] = l_w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) red[wave][lane][e] = acc[g][e];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (int i = lane; i < D; i += 64) {
+            const int c = i / 8, e = i % 8;
+            float sum = 0.0f;
+            for (int r = 0; r < R; r++) sum += red[wave][r * LPK + c][e];
+            wsum[wave][g][i] = sum;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+        const int g = i / D, d = i % D;
+        float M = -INFINITY;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+        float accv = 0.0f, lv = 0.0f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < 4; w++) {
+                const float f = (wm[w][g] == -INFINITY) ? 0.0f : exp2f(wm[w][g] - M);
+                accv += f * wsum[w][g][d];
+                lv += f * wlsum[w][g];
+            }
+        }
+        float* dst = ws + ((int64_t)(bhq0 + g) * n_splits + split) * (D + 2);
+        dst[2 + d] = accv;
+        if (d == 0) {
+            dst[0] = M;
+            dst[1] = lv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- binary scores
+// One lane per key; exact fp32 score (scale_q*scale_k)*(2pc-d) * (1/sqrt(d)).
+template <int D>
+__global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlanes kb, float* scores,
+                                                    int32_t* pcs, int Hq, int Hkv, int S,
+                                                    int kv_stride) {
+    __shared__ uint32_t qs[D / 32];
+    __shared__ float sq;
+    const int bh = blockIdx.y;
+    const int b = bh / Hq, h = bh % Hq;
+    const int kvh = h / (Hq / Hkv);
+    const uint16_t* qb = q + (int64_t)bh * D;
+    if (threadIdx.x < D / 32) {
+        uint32_t bits = 0;
+        for (int i = 0; i < 32; i++) bits |= (h2f(qb[32 * threadIdx.x + i]) >= 0.0f ? 1u : 0u) << i;
+        qs[threadIdx.x] = bits;
+    }
+    if (threadIdx.x == 0) {
+        float acc = 0.0f;
+        for (int i = 0; i < D; i++) acc += fabsf(h2f(qb[i]));  // sequential (src/compensated_attention.cu:65-67)
+        sq = acc / (float)D;
+    }
+    __syncthreads();
+    const float isd = 1.0f / sqrtf((float)D);
+    const int64_t base = (int64_t)(b * Hkv + kvh) * kv_stride;
+    for (int s = blockIdx.x * blockDim.x + threadIdx.x; s < S; s += gridDim.x * blockDim.x) {
+        const SignWords<D> ks = load_signs<D>(kb.signs + (base + s) * (D / 8));
+        int pc = 0;
+#pragma unroll
+        for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
+        const float xdot = (sq * h2f(kb.scales[base + s])) * (float)(2 * pc - D);
+        if (scores) scores[(int64_t)bh * S + s] = xdot * isd;
+        if (pcs) pcs[(int64_t)bh * S + s] = pc;
+    }
+}
+
+// ---------------------------------------------------------------- entropy
+// src/adaptive_precision.cu:196-313.  Tree-order scale_q (thread t of 128
+// holds |q_t| + |q_{t+128}|, tree s = 64..1), scores without 1/sqrt(d),
+// H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread.
+template <int D>
+__global__ __launch_bounds__(256) void entropy_kernel(const uint16_t* q, BinPlanes kb, float* out,
+                                                     int S) {
+    __shared__ float part[128];
+    __shared__ uint32_t qs[D / 32];
+    __shared__ float sm[256], sz[256], sw[256];
+    const int bh = blockIdx.x;
+    const uint16_t* qb = q + (int64_t)bh * D;
+    const int tid = threadIdx.x;
+    if (tid < 128) {
+        float local = 0.0f;
+        for (int i = tid; i < D; i += 128) local += fabsf(h2f(qb[i]));
+        part[tid] = local;
+    }
+    if (tid < D / 32) {
+        uint32_t bits = 0;
+        for (int i = 0; i < 32; i++) bits |= (h2f(qb[32 * tid + i]) >= 0.0f ? 1u : 0u) << i;
+        qs[tid] = bits;
+    }
+    __syncthreads();
+    for (int st = 64; st > 0; st >>= 1) {
+        if (tid < st) part[tid] += part[tid + st];
+        __syncthreads();
+    }
+    const float sq = part[0] / (float)D;
+    const int64_t base = (int64_t)bh * S;
+    float M = -1e30f, Z = 0.0f, W = 0.0f;
+    for (int s = tid; s < S; s += blockDim.x) {
+        const SignWords<D> ks = load_signs<D>(kb.signs + (base + s) * (D / 8));
+        int pc = 0;
+#pragma unroll
+        for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
+        const float sc = sq * h2f(kb.scales[base + s]) * (float)(2 * pc - D);
+        if (sc > M) {
+            const float f = expf(M - sc);
+            Z *= f;
+            W *= f;
+            M = sc;
+        }
+        const float e = expf(sc - M);
+        Z += e;
+        W += e * sc;
+    }
+    sm[tid] = M;
+    sz[tid] = Z;
+    sw[tid] = W;
+    __syncthreads();
+    if (tid == 0) {
+        float gm = -1e30f;
+        for (int i = 0; i < (int)blockDim.x; i++) gm = fmaxf(gm, sm[i]);
+        float z = 0.0f, w = 0.0f;
+        for (int i = 0; i < (int)blockDim.x; i++) {
+            const float f = expf(sm[i] - gm);
+            z += sz[i] * f;
+            w += sw[i] * f;
+        }
+        out[bh] = (logf(z) + gm) - w / fmaxf(z, 1e-12f);
+    }
+}
+
+__global__ void select_kernel(const float* e, uint8_t* modes, int n, float thr) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) modes[i] = e[i] >= thr ? 0 : 1;  // src/adaptive_precision.cu:133-144
+}
+
+// ---------------------------------------------------------------- host side
+int pick_g(int group) {
+    if (group % 8 == 0) return 8;
+    if (group % 4 == 0) return 4;
+    if (group % 2 == 0) return 2;
+    return 1;
+}
+
+struct SplitPlan {
+    int n_splits, chunk, G;
+};
+
+SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
+    SplitPlan p;
+    p.G = pick_g(hq / hkv);
+    const int groups = batch * hkv * ((hq / hkv) / p.G);
+    const int tiles = (S + 63) / 64;
+    const int cu = bc::device_cu_count();
+    int want = (4 * cu + groups - 1) / groups;   // aim for ~4 workgroups per CU
+    int max_split = (tiles + 7) / 8;             // at least 8 tiles (2 per wave) per split
+    if (max_split < 1) max_split = 1;
+    if (want > max_split) want = max_split;
+    if (want < 1) want = 1;
+    const int tiles_per = (tiles + want - 1) / want;
+    p.chunk = tiles_per * 64;
+    p.n_splits = tiles == 0 ? 1 : (tiles + tiles_per - 1) / tiles_per;
+    return p;
+}
+
+size_t ws_bytes(int batch, int hq, int hkv, int S, int D) {
+    SplitPlan p = plan_splits(batch, hq, hkv, S);
+    return (size_t)batch * hq * p.n_splits * (D + 2) * sizeof(float);
+}
+
+int validate_heads(int batch, int n_heads, int n_kv_heads, int seq_len, int kv_stride, int d) {
+    BC_REQUIRE(bc::head_dim_ok(d), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", d);
+    BC_REQUIRE(batch >= 0 && n_heads >= 0 && n_kv_heads > 0 && seq_len >= 0, BC_ERR_INVALID_ARGUMENT,
+               "invalid dims batch=%d n_heads=%d n_kv_heads=%d seq_len=%d", batch, n_heads,
+               n_kv_heads, seq_len);
+    BC_REQUIRE(n_heads % n_kv_heads == 0, BC_ERR_INVALID_ARGUMENT,
+               "n_heads (%d) must be a multiple of n_kv_heads (%d)", n_heads, n_kv_heads);
+    BC_REQUIRE(kv_stride >= seq_len, BC_ERR_INVALID_ARGUMENT, "kv_stride (%d) < seq_len (%d)",
+               kv_stride, seq_len);
+    return BC_OK;
+}
+
+template <int D, int G>
+void launch_split(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
+    if (mode == MODE_BINARY)
+        hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_BINARY>), grid, dim3(256), 0, st, a);
+    else if (mode == MODE_COMP)
+        hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_COMP>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_ADAPTIVE>), grid, dim3(256), 0, st, a);
+}
+
+template <int D>
+void launch_split_g(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
+    switch (G) {
+        case 8: launch_split<D, 8>(mode, a, grid, st); break;
+        case 4: launch_split<D, 4>(mode, a, grid, st); break;
+        case 2: launch_split<D, 2>(mode, a, grid, st); break;
+        default: launch_split<D, 1>(mode, a, grid, st); break;
+    }
+}
+
+template <int D>
+void launch_combine(const float* ws, uint16_t* out, int bh, int n_splits, hipStream_t st) {
+    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(bh), dim3(D < 256 ? D : 256), 0, st, ws, out,
+                       n_splits);
+}
+
+#define BC_DISPATCH_D(d, FN, ...)                                           \
+    switch (d) {                                                            \
+        case 32: FN<32>(__VA_ARGS__); break;                                \
+        case 64: FN<64>(__VA_ARGS__); break;                                \
+        case 96: FN<96>(__VA_ARGS__); break;                                \
+        case 128: FN<128>(__VA_ARGS__); break;                              \
+        case 160: FN<160>(__VA_ARGS__); break;                              \
+        case 192: FN<192>(__VA_ARGS__); break;                              \
+        case 224: FN<224>(__VA_ARGS__); break;                              \
+        case 256: FN<256>(__VA_ARGS__); break;                              \
+        default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", d); \
+    }
+
+}  // namespace
+
+namespace bc {
+
+// Phase 1 (split partials into the workspace) and phase 2 (combine).  Shared
+// by the public entry points and the adaptive driver (adaptive.hip).
+int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
+                int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
+                hipStream_t st, const uint32_t* thresh, const int32_t* need,
+                const int32_t* tie_prefix, uint8_t* selected) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin && v_bin, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    BC_REQUIRE(mode == MODE_BINARY || (k_res && v_res), BC_ERR_INVALID_ARGUMENT,
+               "residual blobs required");
+    const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
+               "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
+    AttnArgs a{};
+    a.q = (const uint16_t*)q;
+    a.kb = bin_planes(k_bin, cap, head_dim);
+    a.vb = bin_planes(v_bin, cap, head_dim);
+    if (k_res) a.kr = res_planes(k_res, cap, head_dim);
+    if (v_res) a.vr = res_planes(v_res, cap, head_dim);
+    a.B = batch;
+    a.Hq = n_heads;
+    a.Hkv = n_kv_heads;
+    a.S = seq_len;
+    a.kv_stride = kv_stride;
+    a.n_splits = p.n_splits;
+    a.chunk = p.chunk;
+    a.ws = (float*)workspace;
+    a.thresh = thresh;
+    a.need = need;
+    a.tie_prefix = tie_prefix;
+    a.n_tiles = (seq_len + 63) / 64;
+    a.selected = selected;
+    const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
+    BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
+    return bc::check_launch("attention split");
+}
+
+int run_combine(const void* workspace, void* out, int batch, int n_heads, int n_kv_heads,
+                int seq_len, int head_dim, hipStream_t st) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(workspace && out, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    BC_DISPATCH_D(head_dim, launch_combine, (const float*)workspace, (uint16_t*)out,
+                  batch * n_heads, p.n_splits, st);
+    return bc::check_launch("attention combine");
+}
+
+int run_attention(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                  const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
+                  int seq_len, int kv_stride, int head_dim, void* workspace,
+                  size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
+                  const int32_t* need, const int32_t* tie_prefix, uint8_t* selected) {
+    int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
+                         kv_stride, head_dim, workspace, workspace_bytes, st, thresh, need,
+                         tie_prefix, selected);
+    if (rc != BC_OK) return rc;
+    BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
+               "null output");
+    return run_combine(workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim, st);
+}
+
+size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d) {
+    return ws_bytes(batch, n_heads, n_kv_heads, seq_len, d);
+}
+
+}  // namespace bc
+
+extern "C" int bc_attention_workspace_size(int batch, int n_heads, int n_kv_heads, int seq_len,
+                                           int head_dim, size_t* bytes) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
+    if (v != BC_OK) return v;
+    BC_REQUIRE(bytes != nullptr, BC_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    return BC_OK;
+}
+
+extern "C" int bc_attention_partial(const void* q, const void* k_bin, const void* k_res,
+                                    const void* v_bin, const void* v_res, int batch, int n_heads,
+                                    int n_kv_heads, int seq_len, int kv_stride, int head_dim,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+    BC_REQUIRE((k_res == nullptr) == (v_res == nullptr), BC_ERR_INVALID_ARGUMENT,
+               "k_res and v_res must both be given or both be null");
+    return bc::run_partial(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, batch,
+                           n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
+                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr,
+                           nullptr);
+}
+
+extern "C" int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads,
+                                    int n_kv_heads, int seq_len, int head_dim, void* stream) {
+    return bc::run_combine(workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim,
+                           (hipStream_t)stream);
+}
+
+extern "C" int bc_binary_attention(const void* q, const void* k_bin, const void* v_bin, void* out,
+                                   int batch, int n_heads, int seq_len, int head_dim,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    return bc::run_attention(MODE_BINARY, q, k_bin, nullptr, v_bin, nullptr, out, batch, n_heads,
+                             n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
+                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+extern "C" int bc_compensated_attention(const void* q, const void* k_bin, const void* k_res,
+                                        const void* v_bin, const void* v_res, void* out, int batch,
+                                        int n_heads, int seq_len, int head_dim, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    return bc::run_attention(MODE_COMP, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads,
+                             n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
+                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_res,
+                                const void* v_bin, const void* v_res, void* out, int batch,
+                                int n_heads, int n_kv_heads, int seq_len, int kv_stride,
+                                int head_dim, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    BC_REQUIRE((k_res == nullptr) == (v_res == nullptr), BC_ERR_INVALID_ARGUMENT,
+               "k_res and v_res must both be given or both be null");
+    return bc::run_attention(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, out,
+                             batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
+                             workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr,
+                             nullptr);
+}
+
+template <int D>
+static void launch_scores(const void* q, BinPlanes kb, float* scores, int32_t* pcs, int batch,
+                          int hq, int hkv, int S, int stride, hipStream_t st) {
+    const int bx = (S + 255) / 256;
+    hipLaunchKernelGGL((scores_kernel<D>), dim3(bx < 1024 ? (bx < 1 ? 1 : bx) : 1024, batch * hq),
+                       dim3(256), 0, st, (const uint16_t*)q, kb, scores, pcs, hq, hkv, S, stride);
+}
+
+extern "C" int bc_binary_scores(const void* q, const void* k_bin, float* scores,
+                                int32_t* popcounts, int batch, int n_heads, int n_kv_heads,
+                                int seq_len, int kv_stride, int head_dim, void* stream) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads * seq_len == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
+    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
+    BC_DISPATCH_D(head_dim, launch_scores, q, kb, scores, popcounts, batch, n_heads, n_kv_heads,
+                  seq_len, kv_stride, (hipStream_t)stream);
+    return bc::check_launch("binary scores");
+}
+
+template <int D>
+static void launch_entropy(const void* q, BinPlanes kb, float* out, int bh, int S, hipStream_t st) {
+    hipLaunchKernelGGL((entropy_kernel<D>), dim3(bh), dim3(256), 0, st, (const uint16_t*)q, kb,
+                       out, S);
+}
+
+extern "C" int bc_compute_head_entropy(const void* q, const void* k_bin, float* entropy,
+                                       int batch, int n_heads, int seq_len, int head_dim,
+                                       void* stream) {
+    int v = validate_heads(batch, n_heads, n_heads > 0 ? n_heads : 1, seq_len, seq_len, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin && entropy, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const int64_t cap = (int64_t)batch * n_heads * seq_len;
+    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
+    BC_DISPATCH_D(head_dim, launch_entropy, q, kb, entropy, batch * n_heads, seq_len,
+                  (hipStream_t)stream);
+    return bc::check_launch("entropy");
+}
+
+extern "C" int bc_adaptive_select(const float* entropy, uint8_t* modes, int batch, int n_heads,
+                                  float threshold, void* stream) {
+    BC_REQUIRE(batch >= 0 && n_heads >= 0, BC_ERR_INVALID_ARGUMENT, "negative dims");
+    const int n = batch * n_heads;
+    if (n == 0) return BC_OK;
+    BC_REQUIRE(entropy && modes, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    hipLaunchKernelGGL(select_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       entropy, modes, n, threshold);
+    return bc::check_launch("adaptive select");
+}
+
+template <int D>
+static void launch_ref(int G, const void* q, const void* k, const void* v, int hq, int hkv, int S,
+                       int ns, int chunk, float* ws, dim3 grid, hipStream_t st) {
+    const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
+    switch (G) {
+        case 8: hipLaunchKernelGGL((ref_split_kernel<D, 8>), grid, dim3(256), 0, st, qq, kk, vv, hq, hkv, S, ns, chunk, ws); break;
+        case 4: hipLaunchKernelGGL((ref_split_kernel<D, 4>), grid, dim3(256), 0, st, qq, kk, vv, hq, hkv, S, ns, chunk, ws); break;
+        case 2: hipLaunchKernelGGL((ref_split_kernel<D, 2>), grid, dim3(256), 0, st, qq, kk, vv, hq, hkv, S, ns, chunk, ws); break;
+        default: hipLaunchKernelGGL((ref_split_kernel<D, 1>), grid, dim3(256), 0, st, qq, kk, vv, hq, hkv, S, ns, chunk, ws); break;
+    }
+}
+
+extern "C" int bc_reference_attention(const void* q, const void* k, const void* v, void* out,
+                                      int batch, int n_heads, int n_kv_heads, int seq_len,
+                                      int head_dim, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    int vv = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
+    if (vv != BC_OK) return vv;
+    BC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, BC_ERR_UNSUPPORTED,
+               "reference attention supports head_dim 64, 128 or 256, got %d", head_dim);
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k && v && out, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
+               "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
+    hipStream_t st = (hipStream_t)stream;
+    switch (head_dim) {
+        case 64: launch_ref<64>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
+        case 128: launch_ref<128>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
+        case 256: launch_ref<256>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
+        default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
+    }
+    int rc = bc::check_launch("reference attention");
+    if (rc != BC_OK) return rc;
+    BC_DISPATCH_D(head_dim, launch_combine, (const float*)workspace, (uint16_t*)out,
+                  batch * n_heads, p.n_splits, st);
+    return bc::check_launch("reference combine");
+}

@@ -1,0 +1,109 @@
+// Shared device/host helpers for the bitcache gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bitcache.h"
+
+#define BC_WAVE 64
+#define BC_MAX_HEAD_DIM 256
+
+// ---------------------------------------------------------------- error state
+namespace bc {
+
+int set_error(int status, const char* fmt, ...);
+int check_launch(const char* what);
+
+inline bool head_dim_ok(int d) { return d >= 32 && d <= BC_MAX_HEAD_DIM && (d % 32) == 0; }
+
+// CU count of the current device (cached per device).
+int device_cu_count();
+
+}  // namespace bc
+
+#define BC_REQUIRE(cond, status, ...)                   \
+    do {                                                \
+        if (!(cond)) return bc::set_error(status, __VA_ARGS__); \
+    } while (0)
+
+// ---------------------------------------------------------------- blob layout
+// Dense planar blob of capacity n vectors (see include/bitcache.h).
+struct BinPlanes {
+    const uint8_t* signs;    // n * d/8 bytes
+    const uint16_t* scales;  // n fp16
+};
+struct ResPlanes {
+    const uint8_t* codes;    // n * d/2 bytes
+    const uint16_t* scales;  // n fp16
+};
+
+__host__ __device__ inline BinPlanes bin_planes(const void* blob, int64_t cap, int d) {
+    const uint8_t* p = (const uint8_t*)blob;
+    return BinPlanes{p, (const uint16_t*)(p + cap * (d / 8))};
+}
+__host__ __device__ inline ResPlanes res_planes(const void* blob, int64_t cap, int d) {
+    const uint8_t* p = (const uint8_t*)blob;
+    return ResPlanes{p, (const uint16_t*)(p + cap * (d / 2))};
+}
+
+// ---------------------------------------------------------------- device helpers
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, h);
+    return (float)v;
+}
+// round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 in the default rounding mode)
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, BC_WAVE));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, BC_WAVE);
+    return v;
+}
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// Sign-word loaders: D/8 bytes per vector, returned as D/32 uint32 words.
+template <int D>
+struct SignWords {
+    uint32_t w[D / 32];
+};
+template <int D>
+__device__ __forceinline__ SignWords<D> load_signs(const uint8_t* p) {
+    // D/8 bytes at a D/8-byte aligned address: 16-byte loads where the stride allows
+    SignWords<D> s;
+    if constexpr (D % 128 == 0) {
+#pragma unroll
+        for (int i = 0; i < D / 128; i++) {
+            uint4 v = ((const uint4*)p)[i];
+            s.w[4 * i + 0] = v.x; s.w[4 * i + 1] = v.y; s.w[4 * i + 2] = v.z; s.w[4 * i + 3] = v.w;
+        }
+    } else if constexpr (D % 64 == 0) {
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) {
+            uint2 v = ((const uint2*)p)[i];
+            s.w[2 * i + 0] = v.x; s.w[2 * i + 1] = v.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) s.w[i] = ((const uint32_t*)p)[i];
+    }
+    return s;
+}
+
+// Order-preserving map of an fp32 key to uint32 (larger float -> larger uint).
+// -0 is folded into +0 and NaN into -inf before the map.
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+    f = f + 0.0f;
+    if (!(f == f)) f = -INFINITY;
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+

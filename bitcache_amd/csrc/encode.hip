@@ -1,0 +1,293 @@
+// Encode kernels: fp16 vectors -> sign bits + fp16 mean-|x| scale (+ INT4 residual).
+//
+// One wave64 encodes one vector.  Lane l holds elements l + 64k (k < D/64),
+// which makes the sign words two (or one) wave ballots and lets the scale be
+// reduced in exactly the reference's fp32 order: the reference block has 128
+// threads, thread t summing |x_t| + |x_{t+128}| (src/binary_encode.cu:70-80),
+// followed by a shared-memory tree p[t] += p[t+s], s = 64..1 (:83-88).  Lane l
+// plays threads l and l+64; the s = 64 step is an in-lane add and the s = 32..1
+// steps are an xor butterfly whose lane-0 value follows the tree's association
+// exactly (fp32 addition is commutative).
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+enum EncodeMode : int {
+    ENC_BINARY = 0,         // bits + scale
+    ENC_FUSED_FP16 = 1,     // bits + scale + residual against the fp16 scale (two-step semantics)
+    ENC_FUSED_FP32 = 2,     // bits + scale + residual against the fp32 mean (online semantics)
+    ENC_RESIDUAL_ONLY = 3,  // residual against bits + fp16 scale read from a binary blob
+};
+
+struct EncodeJob {
+    const uint16_t* src;          // [n, D] fp16
+    uint8_t* sign_plane;          // destination binary planes (ENC_RESIDUAL_ONLY: source)
+    uint16_t* scale_plane;
+    uint8_t* code_plane;          // destination residual planes (may be null)
+    uint16_t* rscale_plane;
+    int64_t n;                    // vectors in this job
+    // destination vector index = (v / row_len) * row_stride + row_offset + v % row_len
+    int64_t row_len, row_stride, row_offset;
+};
+
+// __float2int_rn followed by the [-7, 7] clamp of src/residual.cu:237-242; NaN -> 0.
+__device__ __forceinline__ int quant7(float v) {
+    if (!(v == v)) return 0;
+    float c = fminf(fmaxf(v, -7.0f), 7.0f);
+    return (int)__builtin_rintf(c);
+}
+
+template <int D, int MODE>
+__global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1) {
+    constexpr int K = (D + 63) / 64;  // elements per lane
+    const int lane = threadIdx.x & 63;
+    const int64_t total = j0.n + j1.n;
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
+    for (int64_t gv = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6); gv < total;
+         gv += nwaves) {
+        const bool second = gv >= j0.n;
+        const EncodeJob& J = second ? j1 : j0;
+        const int64_t v = second ? gv - j0.n : gv;
+        const int64_t dv = (v / J.row_len) * J.row_stride + J.row_offset + v % J.row_len;
+
+        float x[K];
+        bool active[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int e = lane + 64 * k;
+            active[k] = e < D;
+            x[k] = active[k] ? h2f(J.src[v * D + e]) : 0.0f;
+        }
+
+        float scale_for_residual;
+        uint64_t bits[K];
+        if constexpr (MODE == ENC_RESIDUAL_ONLY) {
+            const uint32_t* sp = (const uint32_t*)(J.sign_plane + dv * (D / 8));
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const uint64_t lo = sp[2 * k];
+                const uint64_t hi = (2 * k + 1 < D / 32) ? sp[2 * k + 1] : 0u;
+                bits[k] = lo | (hi << 32);
+            }
+            scale_for_residual = h2f(J.scale_plane[dv]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                // x >= 0.0f: +-0 -> 1, NaN -> 0 (src/binary_encode.cu:74)
+                bits[k] = __ballot(active[k] && x[k] >= 0.0f);
+            }
+            // tree-order abs sum (see file comment).  Lane l is thread l (elements
+            // l, l+128) and thread l+64 (elements l+64, l+192); absent elements
+            // are 0 and adding them is exact.
+            float pA = 0.0f + fabsf(x[0]);
+            if constexpr (K > 2) pA = pA + fabsf(x[2]);
+            float pB = 0.0f;
+            if constexpr (K > 1) pB = pB + fabsf(x[1]);
+            if constexpr (K > 3) pB = pB + fabsf(x[3]);
+            float p = pA + pB;
+#pragma unroll
+            for (int s = 32; s > 0; s >>= 1) p = p + __shfl_xor(p, s, 64);
+            const float total_abs =
+                __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, p)));
+            const float mean = total_abs / (float)D;
+            if (lane == 0) J.scale_plane[dv] = f2h(mean);
+            // sign words: D/32 little-endian uint32 words per vector
+            uint32_t* sp = (uint32_t*)(J.sign_plane + dv * (D / 8));
+            if (lane < D / 32) {
+                uint64_t w = bits[0];
+#pragma unroll
+                for (int k = 1; k < K; k++) w = ((lane >> 1) == k) ? bits[k] : w;
+                sp[lane] = (lane & 1) ? (uint32_t)(w >> 32) : (uint32_t)w;
+            }
+            if constexpr (MODE == ENC_FUSED_FP16) scale_for_residual = h2f(f2h(mean));
+            else scale_for_residual = mean;
+        }
+
+        if constexpr (MODE != ENC_BINARY) {
+            if (J.code_plane == nullptr) continue;
+            const float s = scale_for_residual;
+            float r[K];
+            float m = 0.0f;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const bool b = (bits[k] >> lane) & 1ull;
+                r[k] = x[k] - (b ? s : -s);
+                if (active[k]) m = fmaxf(m, fabsf(r[k]));
+            }
+            // fmaxf ignores NaN and is order independent: a butterfly gives the
+            // reference's absmax (src/residual.cu:201-223) in every lane.
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            const float absmax = m;
+            const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
+            if (lane == 0) J.rscale_plane[dv] = f2h(absmax);
+            uint8_t* cp = J.code_plane + dv * (D / 2);
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                // element e = lane + 64k; element 2j -> low nibble of byte j
+                uint32_t c = (uint32_t)quant7(r[k] * inv) & 0xFu;
+                uint32_t byte = c | (__shfl_xor(c, 1, 64) << 4);          // valid on even lanes
+                uint32_t half = byte | (__shfl_xor(byte, 2, 64) << 8);     // lanes % 4 == 0
+                uint32_t word = half | (__shfl_xor(half, 4, 64) << 16);    // lanes % 8 == 0
+                const int e = lane + 64 * k;
+                if ((lane & 7) == 0 && e < D) ((uint32_t*)cp)[e >> 3] = word;
+            }
+        }
+    }
+}
+
+int grid_for(int64_t nvec) {
+    const int64_t want = (nvec + 3) / 4;
+    const int64_t cap = (int64_t)bc::device_cu_count() * 32;
+    return (int)(want < cap ? (want < 1 ? 1 : want) : cap);
+}
+
+template <int MODE>
+int launch_encode(int d, const EncodeJob& a, const EncodeJob& b, hipStream_t st) {
+    const int grid = grid_for(a.n + b.n);
+    switch (d) {
+#define BC_CASE(DD)                                                                       \
+    case DD:                                                                              \
+        hipLaunchKernelGGL((encode_kernel<DD, MODE>), dim3(grid), dim3(256), 0, st, a, b); \
+        break;
+        BC_CASE(32) BC_CASE(64) BC_CASE(96) BC_CASE(128) BC_CASE(160) BC_CASE(192) BC_CASE(224)
+        BC_CASE(256)
+#undef BC_CASE
+        default:
+            return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d unsupported", d);
+    }
+    return bc::check_launch("encode");
+}
+
+EncodeJob make_job(const void* src, void* bin, void* res, int64_t n, int64_t cap, int d,
+                   int64_t row_len, int64_t row_stride, int64_t row_offset) {
+    EncodeJob j{};
+    j.src = (const uint16_t*)src;
+    j.sign_plane = (uint8_t*)bin;
+    j.scale_plane = (uint16_t*)((uint8_t*)bin + cap * (d / 8));
+    if (res) {
+        j.code_plane = (uint8_t*)res;
+        j.rscale_plane = (uint16_t*)((uint8_t*)res + cap * (d / 2));
+    }
+    j.n = n;
+    j.row_len = row_len;
+    j.row_stride = row_stride;
+    j.row_offset = row_offset;
+    return j;
+}
+
+}  // namespace
+
+extern "C" int bc_binary_encode(const void* src, void* binary_blob, int64_t n_vecs, int head_dim,
+                                void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", head_dim);
+    BC_REQUIRE(n_vecs >= 0, BC_ERR_INVALID_ARGUMENT, "n_vecs < 0");
+    if (n_vecs == 0) return BC_OK;
+    BC_REQUIRE(src && binary_blob, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    EncodeJob a = make_job(src, binary_blob, nullptr, n_vecs, n_vecs, head_dim, 1, 1, 0);
+    EncodeJob b{};
+    return launch_encode<ENC_BINARY>(head_dim, a, b, (hipStream_t)stream);
+}
+
+extern "C" int bc_residual_encode(const void* src, const void* binary_blob, void* residual_blob,
+                                  int64_t n_vecs, int head_dim, void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", head_dim);
+    BC_REQUIRE(n_vecs >= 0, BC_ERR_INVALID_ARGUMENT, "n_vecs < 0");
+    if (n_vecs == 0) return BC_OK;
+    BC_REQUIRE(src && binary_blob && residual_blob, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    EncodeJob a = make_job(src, (void*)binary_blob, residual_blob, n_vecs, n_vecs, head_dim, 1, 1, 0);
+    EncodeJob b{};
+    return launch_encode<ENC_RESIDUAL_ONLY>(head_dim, a, b, (hipStream_t)stream);
+}
+
+extern "C" int bc_encode_fused(const void* src, void* binary_blob, void* residual_blob,
+                               int64_t n_vecs, int head_dim, int scale_mode, void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", head_dim);
+    BC_REQUIRE(n_vecs >= 0, BC_ERR_INVALID_ARGUMENT, "n_vecs < 0");
+    BC_REQUIRE(scale_mode == 0 || scale_mode == 1, BC_ERR_INVALID_ARGUMENT,
+               "scale_mode must be 0 or 1");
+    if (n_vecs == 0) return BC_OK;
+    BC_REQUIRE(src && binary_blob, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    EncodeJob a = make_job(src, binary_blob, residual_blob, n_vecs, n_vecs, head_dim, 1, 1, 0);
+    EncodeJob b{};
+    if (!residual_blob) return launch_encode<ENC_BINARY>(head_dim, a, b, (hipStream_t)stream);
+    if (scale_mode == 0) return launch_encode<ENC_FUSED_FP16>(head_dim, a, b, (hipStream_t)stream);
+    return launch_encode<ENC_FUSED_FP32>(head_dim, a, b, (hipStream_t)stream);
+}
+
+static int online_common(const void* k, const void* v, void* k_bin, void* k_res, void* v_bin,
+                         void* v_res, int batch, int n_heads, int head_dim, int64_t current_len,
+                         int max_seq, void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", head_dim);
+    BC_REQUIRE(batch >= 0 && n_heads >= 0, BC_ERR_INVALID_ARGUMENT, "negative batch/n_heads");
+    BC_REQUIRE(max_seq > 0, BC_ERR_INVALID_ARGUMENT, "max_seq must be > 0");
+    BC_REQUIRE(current_len >= 0, BC_ERR_INVALID_ARGUMENT, "current_len must be >= 0");
+    const int64_t bh = (int64_t)batch * n_heads;
+    if (bh == 0) return BC_OK;
+    BC_REQUIRE(k && k_bin, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    BC_REQUIRE(!v || v_bin, BC_ERR_INVALID_ARGUMENT, "null V cache");
+    const int64_t cap = bh * max_seq;
+    const int64_t slot = current_len % max_seq;  // src/online_encode.cu:139
+    // binary-only caches (null residual) take the residual-free path
+    const bool res = k_res != nullptr && (!v || v_res != nullptr);
+    EncodeJob a = make_job(k, k_bin, res ? k_res : nullptr, bh, cap, head_dim, 1, max_seq, slot);
+    EncodeJob b{};
+    if (v) b = make_job(v, v_bin, res ? v_res : nullptr, bh, cap, head_dim, 1, max_seq, slot);
+    if (!res && (k_res || (v && v_res))) {
+        // mixed: one side has a residual cache, the other not -> two launches
+        EncodeJob e{};
+        EncodeJob ak = make_job(k, k_bin, k_res, bh, cap, head_dim, 1, max_seq, slot);
+        int st = k_res ? launch_encode<ENC_FUSED_FP32>(head_dim, ak, e, (hipStream_t)stream)
+                       : launch_encode<ENC_BINARY>(head_dim, ak, e, (hipStream_t)stream);
+        if (st != BC_OK || !v) return st;
+        EncodeJob av = make_job(v, v_bin, v_res, bh, cap, head_dim, 1, max_seq, slot);
+        return v_res ? launch_encode<ENC_FUSED_FP32>(head_dim, av, e, (hipStream_t)stream)
+                     : launch_encode<ENC_BINARY>(head_dim, av, e, (hipStream_t)stream);
+    }
+    if (res) return launch_encode<ENC_FUSED_FP32>(head_dim, a, b, (hipStream_t)stream);
+    return launch_encode<ENC_BINARY>(head_dim, a, b, (hipStream_t)stream);
+}
+
+extern "C" int bc_online_encode_token(const void* kv, void* binary_cache, void* residual_cache,
+                                      int batch, int n_heads, int head_dim, int64_t current_len,
+                                      int max_seq, void* stream) {
+    return online_common(kv, nullptr, binary_cache, residual_cache, nullptr, nullptr, batch,
+                         n_heads, head_dim, current_len, max_seq, stream);
+}
+
+extern "C" int bc_online_encode_kv(const void* k, const void* v, void* k_bin, void* k_res,
+                                   void* v_bin, void* v_res, int batch, int n_heads, int head_dim,
+                                   int64_t current_len, int max_seq, void* stream) {
+    BC_REQUIRE(v != nullptr, BC_ERR_INVALID_ARGUMENT, "null V");
+    return online_common(k, v, k_bin, k_res, v_bin, v_res, batch, n_heads, head_dim, current_len,
+                         max_seq, stream);
+}
+
+extern "C" int bc_encode_into_cache(const void* src, void* binary_cache, void* residual_cache,
+                                    int64_t rows, int seq, int head_dim, int start_pos,
+                                    int max_seq, int scale_mode, void* stream) {
+    BC_REQUIRE(bc::head_dim_ok(head_dim), BC_ERR_UNSUPPORTED,
+               "head_dim must be a multiple of 32 in [32, 256], got %d", head_dim);
+    BC_REQUIRE(rows >= 0 && seq >= 0 && start_pos >= 0 && max_seq > 0, BC_ERR_INVALID_ARGUMENT,
+               "invalid dims");
+    BC_REQUIRE((int64_t)start_pos + seq <= max_seq, BC_ERR_INVALID_ARGUMENT,
+               "start_pos + seq (%d) exceeds max_seq (%d)", start_pos + seq, max_seq);
+    BC_REQUIRE(scale_mode == 0 || scale_mode == 1, BC_ERR_INVALID_ARGUMENT,
+               "scale_mode must be 0 or 1");
+    if (rows * seq == 0) return BC_OK;
+    BC_REQUIRE(src && binary_cache, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const int64_t cap = rows * max_seq;
+    EncodeJob a = make_job(src, binary_cache, residual_cache, rows * seq, cap, head_dim, seq,
+                           max_seq, start_pos);
+    EncodeJob b{};
+    hipStream_t st = (hipStream_t)stream;
+    if (!residual_cache) return launch_encode<ENC_BINARY>(head_dim, a, b, st);
+    if (scale_mode == 0) return launch_encode<ENC_FUSED_FP16>(head_dim, a, b, st);
+    return launch_encode<ENC_FUSED_FP32>(head_dim, a, b, st);
+}

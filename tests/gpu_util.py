@@ -1,0 +1,68 @@
+"""Helpers shared by the GPU parity tests: blob -> oracle semantic arrays and
+the output tolerance of the compressed path."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+# north_star tolerance for fp16/fp32 outputs: max-abs error relative to the
+# largest reference magnitude <= 2e-3 and cosine similarity >= 0.9999.
+REL_TOL = 2e-3
+COS_TOL = 0.9999
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def bin_from_blob(blob: torch.Tensor, n: int, d: int) -> O.BinaryEnc:
+    b = to_np(blob)
+    sb = n * d // 8
+    words = b[:sb].view("<u4").reshape(n, d // 32).astype(np.uint32)
+    scale = b[sb:sb + 2 * n].view(np.float16).copy()
+    return O.BinaryEnc(words=words, scale=scale, mean32=scale.astype(np.float32))
+
+
+def res_from_blob(blob: torch.Tensor, n: int, d: int) -> O.ResidualEnc:
+    b = to_np(blob)
+    cb = n * d // 2
+    nib = b[:cb].reshape(n, d // 2)
+    scale = b[cb:cb + 2 * n].view(np.float16).copy()
+    return O.ResidualEnc(codes=O.unpack_nibbles(nib), scale=scale)
+
+
+def slice_enc(e, lo, hi):
+    if isinstance(e, O.BinaryEnc):
+        return O.BinaryEnc(e.words[lo:hi], e.scale[lo:hi], e.mean32[lo:hi])
+    return O.ResidualEnc(e.codes[lo:hi], e.scale[lo:hi])
+
+
+def assert_same_bin(got: O.BinaryEnc, exp: O.BinaryEnc, what=""):
+    assert np.array_equal(got.words, exp.words), f"sign words differ {what}"
+    assert np.array_equal(got.scale.view(np.uint16), exp.scale.view(np.uint16)), f"scales differ {what}"
+
+
+def assert_same_res(got: O.ResidualEnc, exp: O.ResidualEnc, what=""):
+    assert np.array_equal(got.codes, exp.codes), f"codes differ {what}"
+    assert np.array_equal(got.scale.view(np.uint16), exp.scale.view(np.uint16)), f"rscales differ {what}"
+
+
+def close(got: np.ndarray, ref: np.ndarray, rel=REL_TOL, cos=COS_TOL, what=""):
+    g = np.asarray(got, np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    assert np.all(np.isfinite(g)), f"non-finite output {what}"
+    scale = max(np.max(np.abs(r)), 1e-30)
+    err = np.max(np.abs(g - r)) / scale
+    c = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-300))
+    assert err <= rel, f"max-abs rel err {err:.3e} > {rel} {what}"
+    assert c >= cos, f"cosine {c:.6f} < {cos} {what}"
+    return err, c

@@ -1,0 +1,122 @@
+"""CPU checks of the C ABI and the extension boundary (no GPU work is issued):
+the library loads, exports every function include/bitcache.h declares, reports
+the reference's struct sizes, and rejects invalid arguments with the right
+status before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bitcache.h")
+LIB = os.path.join(ROOT, "bitcache_amd", "libbitcache_hip.so")
+
+BC_OK, BC_ERR_INVALID_ARGUMENT, BC_ERR_UNSUPPORTED, BC_ERR_WORKSPACE, BC_ERR_HIP = range(5)
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bc_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.skip("libbitcache_hip.so not built (run python -m bitcache_amd.build)")
+    L = ctypes.CDLL(LIB)
+    L.bc_status_string.restype = ctypes.c_char_p
+    L.bc_last_error.restype = ctypes.c_char_p
+    L.bc_sizeof_binary_vec.restype = ctypes.c_int64
+    L.bc_sizeof_residual_vec.restype = ctypes.c_int64
+    return L
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_sizes_and_strings(lib):
+    assert lib.bc_sizeof_binary_vec() == 36
+    assert lib.bc_sizeof_residual_vec() == 130
+    assert lib.bc_abi_version() == 1
+    assert lib.bc_status_string(BC_OK) == b"ok"
+    assert lib.bc_status_string(BC_ERR_WORKSPACE) == b"workspace too small"
+
+
+def test_encode_argument_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    f = lib.bc_binary_encode
+    f.argtypes = [P, P, ctypes.c_int64, ctypes.c_int, P]
+    assert f(fake, fake, 10, 48, None) == BC_ERR_UNSUPPORTED
+    assert b"multiple of 32" in lib.bc_last_error()
+    assert f(fake, fake, 10, 288, None) == BC_ERR_UNSUPPORTED
+    assert f(fake, fake, -1, 128, None) == BC_ERR_INVALID_ARGUMENT
+    assert f(None, fake, 10, 128, None) == BC_ERR_INVALID_ARGUMENT
+    assert f(None, None, 0, 128, None) == BC_OK          # empty input: nothing to do
+    g = lib.bc_encode_fused
+    g.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P]
+    assert g(fake, fake, fake, 10, 128, 7, None) == BC_ERR_INVALID_ARGUMENT
+    h = lib.bc_online_encode_token
+    h.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int, P]
+    assert h(fake, fake, fake, 1, 1, 128, 0, 0, None) == BC_ERR_INVALID_ARGUMENT   # max_seq 0
+    assert h(fake, fake, fake, 1, 1, 128, -1, 4, None) == BC_ERR_INVALID_ARGUMENT  # current_len < 0
+    e = lib.bc_encode_into_cache
+    e.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_int, P]
+    assert e(fake, fake, fake, 2, 10, 128, 8, 16, 1, None) == BC_ERR_INVALID_ARGUMENT  # overflows ring
+
+
+def test_attention_argument_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    size_t = ctypes.c_size_t
+    ws = lib.bc_attention_workspace_size
+    ws.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(size_t)]
+    n = size_t(0)
+    assert ws(8, 32, 32, 65536, 128, ctypes.byref(n)) == BC_OK and n.value > 0
+    assert ws(1, 6, 4, 10, 128, ctypes.byref(n)) == BC_ERR_INVALID_ARGUMENT   # 6 % 4 != 0
+    assert ws(1, 4, 4, 10, 100, ctypes.byref(n)) == BC_ERR_UNSUPPORTED
+    g = lib.bc_attention_gqa
+    g.argtypes = [P] * 6 + [ctypes.c_int] * 6 + [P, size_t, P]
+    # workspace too small is rejected before any launch
+    assert g(fake, fake, fake, fake, fake, fake, 1, 4, 4, 100, 100, 128, fake, 1, None) == BC_ERR_WORKSPACE
+    assert g(fake, fake, fake, fake, fake, fake, 1, 4, 4, 100, 50, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
+    assert g(fake, fake, fake, fake, None, fake, 1, 4, 4, 100, 100, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
+    a = lib.bc_adaptive_attention
+    a.argtypes = [P] * 7 + [ctypes.c_int] * 7 + [P, size_t, P]
+    assert a(fake, fake, fake, fake, fake, fake, None, 1, 4, 4, 100, 100, 128, -1, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
+    r = lib.bc_reference_attention
+    r.argtypes = [P] * 4 + [ctypes.c_int] * 5 + [P, size_t, P]
+    assert r(fake, fake, fake, fake, 1, 4, 4, 100, 96, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
+
+
+def test_extension_rejects_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    import bitcache_amd
+    if not bitcache_amd._HAS_EXTENSION:
+        pytest.skip("extension not built")
+    import bitcache_amd.functional as F
+    x = torch.zeros((4, 128), dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        F.encode(x)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        bitcache_amd._C.binary_encode(x)
+    with pytest.raises(RuntimeError):
+        bitcache_amd.BitCache(1, 2, 128, 8, device="cpu")
+    assert F.sizeof_binary_vec() == 36 and F.sizeof_residual_vec() == 130
+
+
+def test_product_never_imports_oracle():
+    """The product package must not import, call or read the oracle."""
+    pkg = os.path.join(ROOT, "bitcache_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text.replace("oracles", ""), f"{f} mentions the oracle"

@@ -1,0 +1,107 @@
+"""GPU parity of adaptive top-k residual selection: selected index sets are
+bit-exact with the oracle (stable sort on the exact key, lowest index first on
+ties), outputs within tolerance, and the k = 0 / k = S limits reduce to binary
+and compensated attention."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.gpu_util import bin_from_blob, close, res_from_blob, say, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import bitcache_amd.functional as F
+    return F
+
+
+def make(B, Hq, Hkv, S, d, seed, ties=False):
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((B, Hq, d)) * 0.1).astype(np.float16)
+    k = rng.standard_normal((B, Hkv, S, d)) * 0.1
+    v = rng.standard_normal((B, Hkv, S, d)) * 0.1
+    if ties:
+        # few distinct magnitudes and sign patterns -> many equal keys
+        k = np.sign(k) * 0.125
+        k[..., :100, :] = k[..., 100:200, :] if S >= 200 else k[..., :100, :]
+    return q, k.astype(np.float16), v.astype(np.float16)
+
+
+CASES = [
+    # (B, Hq, Hkv, S, d, top_k, ties)
+    (1, 4, 4, 1000, 128, 100, False),
+    (2, 8, 2, 3000, 128, 300, False),
+    (1, 4, 1, 4097, 64, 410, False),
+    (1, 2, 2, 2000, 128, 200, True),
+    (1, 2, 2, 2000, 128, 1, True),
+    (1, 2, 2, 130, 256, 13, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_adaptive_sets_and_output(F, case):
+    B, Hq, Hkv, S, d, k, ties = case
+    say(f"case adaptive {case}")
+    q, kx, vx = make(B, Hq, Hkv, S, d, seed=S + k, ties=ties)
+    kb, kr = F.encode_fused(torch.from_numpy(kx.reshape(-1, d)).cuda())
+    vb, vr = F.encode_fused(torch.from_numpy(vx.reshape(-1, d)).cuda())
+    out, sel = F.adaptive_attention(torch.from_numpy(q).cuda(), kb, kr, vb, vr, B, Hq, S, d,
+                                    n_kv_heads=Hkv, top_k=k, return_selected=True)
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, ref, sets = O.adaptive_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, k, n_kv_heads=Hkv,
+                                        return_f32=True, return_sets=True)
+    sel = to_np(sel)
+    for (b, h), idx in sets.items():
+        got = np.nonzero(sel[b, h])[0]
+        assert np.array_equal(got, idx), f"selected set differs at (b={b}, h={h})"
+    close(to_np(out).astype(np.float32), ref, what=f"adaptive {case}")
+
+
+def test_adaptive_limits(F):
+    say("case adaptive limits")
+    B, Hq, Hkv, S, d = 1, 4, 2, 700, 128
+    q, kx, vx = make(B, Hq, Hkv, S, d, seed=5)
+    kb, kr = F.encode_fused(torch.from_numpy(kx.reshape(-1, d)).cuda())
+    vb, vr = F.encode_fused(torch.from_numpy(vx.reshape(-1, d)).cuda())
+    qt = torch.from_numpy(q).cuda()
+    a0, s0 = F.adaptive_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv, top_k=0,
+                                  return_selected=True)
+    aS, sS = F.adaptive_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv, top_k=S,
+                                  return_selected=True)
+    assert int(s0.sum()) == 0 and int(sS.sum()) == B * Hq * S
+    b = F.binary_attention(qt, kb, vb, B, Hq, S, d, n_kv_heads=Hkv)
+    c = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
+    close(to_np(a0).astype(np.float32), to_np(b).astype(np.float32), rel=1e-3, what="k=0")
+    close(to_np(aS).astype(np.float32), to_np(c).astype(np.float32), rel=1e-3, what="k=S")
+
+
+def test_config_c5_sample(F):
+    """Config c5 shape on a shortened context (S = 16384, same generator and
+    outlier channels): every selected set of two batches is bit-exact and the
+    output matches the oracle."""
+    from bitcache_amd import workloads as W
+    say("case c5 sample")
+    cfg = W.CONFIGS["c5"]
+    S, d, Hq, Hkv = 16384, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    q, k, v = W.make_qkv(cfg, seq_len=S)
+    q, k, v = q[:2].contiguous(), k[:2].contiguous(), v[:2].contiguous()
+    B = 2
+    kb, kr = F.encode_fused(k.view(-1, d))
+    vb, vr = F.encode_fused(v.view(-1, d))
+    top_k = O.default_top_k(S)
+    out, sel = F.adaptive_attention(q, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv, top_k=top_k,
+                                    return_selected=True)
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, ref, sets = O.adaptive_attention(to_np(q), Kb, Kr, Vb, Vr, B, Hq, S, top_k, n_kv_heads=Hkv,
+                                        return_f32=True, return_sets=True)
+    sel = to_np(sel)
+    for (b, h), idx in sets.items():
+        assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"set differs at {(b, h)}"
+    close(to_np(out).astype(np.float32), ref, what="c5 sample")

@@ -1,0 +1,186 @@
+"""GPU parity of the attention path against the oracle: exact popcounts and
+binary scores, compensated / binary attention within 2e-3 max-abs relative
+error and cosine >= 0.9999, GQA, ring strides, edge sizes, entropy and the
+fp16 reference kernel; plus full-size checks at configs c1, c2 and c3."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.gpu_util import bin_from_blob, close, res_from_blob, say, slice_enc, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def F():
+    import bitcache_amd.functional as F
+    return F
+
+
+def make(B, Hq, Hkv, S, d, seed, scale=0.09, lognorm=0.0):
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((B, Hq, d)) * scale).astype(np.float16)
+    k = rng.standard_normal((B, Hkv, S, d)) * scale
+    v = rng.standard_normal((B, Hkv, S, d)) * scale
+    if lognorm:
+        k = k * np.exp(rng.standard_normal((B, Hkv, S, 1)) * lognorm)
+        v = v * np.exp(rng.standard_normal((B, Hkv, S, 1)) * lognorm)
+    return q, k.astype(np.float16), v.astype(np.float16)
+
+
+def encode_gpu(F, x):
+    xt = torch.from_numpy(np.ascontiguousarray(x.reshape(-1, x.shape[-1]))).cuda()
+    return F.encode_fused(xt)
+
+
+SHAPES = [
+    # (B, Hq, Hkv, S, d)
+    (1, 32, 32, 4096, 128),   # config c1 shape
+    (2, 4, 4, 1, 128),
+    (1, 2, 2, 63, 64),
+    (1, 2, 2, 65, 32),
+    (2, 8, 2, 1000, 128),     # GQA 4
+    (1, 8, 1, 513, 128),      # GQA 8
+    (1, 6, 2, 300, 128),      # GQA 3 (query heads processed one by one)
+    (1, 4, 4, 777, 256),
+    (1, 2, 2, 300, 96),
+    (1, 3, 3, 2000, 160),
+    (1, 2, 2, 129, 192),
+    (1, 2, 2, 200, 224),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[str(s) for s in SHAPES])
+def test_compensated_and_binary_vs_oracle(F, shape):
+    B, Hq, Hkv, S, d = shape
+    say(f"case attention {shape}")
+    q, k, v = make(B, Hq, Hkv, S, d, seed=S + d, lognorm=0.25)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    kw = dict(n_kv_heads=Hkv) if Hkv != Hq else {}
+    out = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, **kw)
+    outb = F.binary_attention(qt, kb, vb, B, Hq, S, d, **kw)
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    _, refb = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    close(to_np(out).astype(np.float32), ref, what=f"compensated {shape}")
+    close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
+
+
+def test_kv_stride_and_zero_length(F):
+    say("case kv_stride")
+    B, H, S, stride, d = 2, 4, 100, 160, 128
+    q, k, v = make(B, H, H, stride, d, seed=3)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    out = F.compensated_attention(qt, kb, kr, vb, vr, B, H, S, d, kv_stride=stride)
+    # oracle on the first S positions of every (b, h)
+    ks, vs = k[:, :, :S], v[:, :, :S]
+    Kb, Kr = O.encode_fused(ks.reshape(-1, d))
+    Vb, Vr = O.encode_fused(vs.reshape(-1, d))
+    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, H, S, return_f32=True)
+    close(to_np(out).astype(np.float32), ref, what="stride")
+    z = F.compensated_attention(qt, kb, kr, vb, vr, B, H, 0, d, kv_stride=stride)
+    assert torch.count_nonzero(z) == 0
+
+
+@pytest.mark.parametrize("gqa", [1, 4])
+def test_binary_scores_exact(F, gqa):
+    say(f"case binary_scores gqa={gqa}")
+    B, Hq, S, d = 2, 8, 1500, 128
+    Hkv = Hq // gqa
+    q, k, _ = make(B, Hq, Hkv, S, d, seed=11)
+    kb = F.encode(torch.from_numpy(k.reshape(-1, d)).cuda())
+    sc, pc = F.binary_scores(torch.from_numpy(q).cuda(), kb, B, Hq, S, d, n_kv_heads=Hkv)
+    Kb = bin_from_blob(kb, B * Hkv * S, d)
+    esc = O.binary_scores(q, Kb, B, Hq, S, n_kv_heads=Hkv)
+    epc = O.binary_popcounts(q, Kb, B, Hq, S, n_kv_heads=Hkv)
+    assert np.array_equal(to_np(pc), epc)
+    assert np.array_equal(to_np(sc).view(np.uint32), esc.view(np.uint32))
+
+
+def test_entropy_vs_oracle(F):
+    say("case entropy")
+    B, H, S, d = 2, 4, 3000, 128
+    q, k, _ = make(B, H, H, S, d, seed=13, scale=0.3)
+    kb = F.encode(torch.from_numpy(k.reshape(-1, d)).cuda())
+    ent = to_np(F.compute_head_entropy(torch.from_numpy(q).cuda(), kb, B, H, S, d))
+    Kb = bin_from_blob(kb, B * H * S, d)
+    ref = O.head_entropy(q, Kb, B, H, S)
+    np.testing.assert_allclose(ent, ref, rtol=2e-4, atol=2e-4)
+    modes = to_np(F.adaptive_select(torch.from_numpy(ent).cuda(), float(np.median(ent))))
+    assert np.array_equal(modes, (ent < np.median(ent)).astype(np.uint8))
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 4, 1000, 128), (2, 8, 2, 777, 64), (1, 2, 2, 64, 256)])
+def test_reference_attention_vs_oracle(F, shape):
+    B, Hq, Hkv, S, d = shape
+    say(f"case reference_attention {shape}")
+    q, k, v = make(B, Hq, Hkv, S, d, seed=17, scale=0.3)
+    out = F.reference_attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
+                                torch.from_numpy(v).cuda(), B, Hq, S, d, n_kv_heads=Hkv)
+    _, ref = O.reference_attention(q, k, v, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    close(to_np(out).astype(np.float32), ref, what="reference")
+
+
+def test_config_c2_full_size_scores(F):
+    """Config c2 at full size: all 8.4M popcounts equal 2*pc-d == sign(q).sign(k)
+    (exact +-1 matmul on the GPU); two heads bit-exact against the oracle, and
+    Kendall tau of binary vs exact scores reported."""
+    from bitcache_amd import workloads as W
+    cfg = W.CONFIGS["c2"]
+    say("case c2 full size")
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, mask = W.make_c2(cfg)
+    kb = F.encode(k.view(-1, d))
+    sc, pc = F.binary_scores(q, kb, B, H, S, d)
+    sq = torch.where(q.float() >= 0, 1.0, -1.0)
+    sk = torch.where(k.float() >= 0, 1.0, -1.0)
+    dots = (sk @ sq[..., None]).squeeze(-1)
+    assert torch.equal((2 * pc - d).float(), dots)
+    Kb = bin_from_blob(kb, B * H * S, d)
+    for (b, h) in [(0, 0), (7, 31)]:
+        Kh = slice_enc(Kb, (b * H + h) * S, (b * H + h + 1) * S)
+        qh = to_np(q[b, h])[None, None]
+        esc = O.binary_scores(qh, Kh, 1, 1, S)
+        assert np.array_equal(to_np(sc[b, h]).view(np.uint32), esc[0, 0].view(np.uint32))
+    # Kendall tau-b of binary scores vs exact q.k on one head (reported, not gated)
+    from scipy.stats import kendalltau
+    exact = (k[0, 0].float() @ q[0, 0].float()).cpu().numpy()
+    tau = kendalltau(to_np(sc[0, 0]), exact).statistic
+    say(f"c2 Kendall tau-b (binary vs exact, head 0): {tau:.4f}")
+    assert tau > 0.2
+
+
+def test_config_c3_full_size(F):
+    """Config c3 at full size (B8 H32 S65536): two (b,h) heads against the
+    oracle; every head against the exact fp16 attention as a quality report."""
+    from bitcache_amd import workloads as W
+    cfg = W.CONFIGS["c3"]
+    say("case c3 full size")
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, v = W.make_qkv(cfg)
+    kb, kr = F.encode_fused(k.view(-1, d))
+    vb, vr = F.encode_fused(v.view(-1, d))
+    out = F.compensated_attention(q, kb, kr, vb, vr, B, H, S, d)
+    torch.cuda.synchronize()
+    for (b, h) in [(0, 0), (5, 17)]:
+        kh = to_np(k[b, h])
+        vh = to_np(v[b, h])
+        Kb, Kr = O.encode_fused(kh)
+        Vb, Vr = O.encode_fused(vh)
+        _, ref = O.compensated_attention(to_np(q[b, h])[None, None], Kb, Kr, Vb, Vr, 1, 1, S,
+                                         return_f32=True)
+        close(to_np(out[b, h]).astype(np.float32), ref[0, 0], what=f"c3 head {(b, h)}")
+    exact = F.reference_attention(q, k, v, B, H, S, d).float()
+    cos = torch.nn.functional.cosine_similarity(out.float().view(-1, d), exact.view(-1, d), dim=1)
+    say(f"c3 compensated vs exact fp16 attention: mean cos {cos.mean().item():.5f} "
+        f"min {cos.min().item():.5f}")
+    assert cos.mean().item() > 0.9

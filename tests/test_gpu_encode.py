@@ -1,0 +1,192 @@
+"""GPU parity: encode kernels are bit-exact with the oracle (sign words, fp16
+scales, INT4 codes and residual scales), for every supported head_dim."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.gpu_util import (assert_same_bin, assert_same_res, bin_from_blob, res_from_blob, say,
+                            to_np)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+ALL_DIMS = (32, 64, 96, 128, 160, 192, 224, 256)
+
+
+@pytest.fixture(scope="module")
+def F():
+    import bitcache_amd.functional as F
+    return F
+
+
+def rand_x(n, d, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n, d)) * rng.lognormal(0, 1.5, (n, 1))).astype(np.float16)
+    x[0] = 0.5
+    x[1, ::2] = np.float16(-0.0)
+    x[2, :3] = [np.inf, -np.inf, np.nan]
+    return x
+
+
+@pytest.mark.parametrize("d", (32, 64, 128, 256))
+def test_encode_golden(F, d):
+    say(f"case encode_golden d={d}")
+    x = GOLDEN[f"enc_d{d}_x"]
+    n = x.shape[0]
+    xt = torch.from_numpy(x).cuda()
+    b = F.encode(xt)
+    r = F.compute_residual(xt, b)
+    got_b = bin_from_blob(b, n, d)
+    assert np.array_equal(got_b.words, GOLDEN[f"enc_d{d}_words"])
+    assert np.array_equal(got_b.scale.view(np.uint16), GOLDEN[f"enc_d{d}_scale"])
+    got_r = res_from_blob(r, n, d)
+    assert np.array_equal(got_r.codes, GOLDEN[f"enc_d{d}_codes"])
+    assert np.array_equal(got_r.scale.view(np.uint16), GOLDEN[f"enc_d{d}_rscale"])
+    b1, r1 = F.encode_fused(xt, fp32_scale=True)
+    got_r1 = res_from_blob(r1, n, d)
+    assert np.array_equal(got_r1.codes, GOLDEN[f"enc_d{d}_codes_online"])
+    assert np.array_equal(got_r1.scale.view(np.uint16), GOLDEN[f"enc_d{d}_rscale_online"])
+    assert torch.equal(b1, b)
+
+
+@pytest.mark.parametrize("d", ALL_DIMS)
+def test_encode_random_all_dims(F, d):
+    say(f"case encode_random d={d}")
+    n = 3001
+    x = rand_x(n, d, d)
+    xt = torch.from_numpy(x).cuda()
+    b = F.encode(xt)
+    r = F.compute_residual(xt, b)
+    eb = O.binary_encode(x)
+    er = O.residual_encode(x, eb)
+    assert_same_bin(bin_from_blob(b, n, d), eb, f"d={d}")
+    assert_same_res(res_from_blob(r, n, d), er, f"d={d}")
+    # fused prefill encode produces identical bytes (the tail of each blob beyond
+    # the payload is untouched scratch and not compared)
+    fb, fr = F.encode_fused(xt, fp32_scale=False)
+    pb, pr = n * (d // 8 + 2), n * (d // 2 + 2)
+    assert torch.equal(fb[:pb], b[:pb]) and torch.equal(fr[:pr], r[:pr])
+    _, on = O.online_encode(x)
+    _, fr1 = F.encode_fused(xt, fp32_scale=True)
+    assert_same_res(res_from_blob(fr1, n, d), on, f"online d={d}")
+
+
+def test_encode_empty_and_single(F):
+    say("case encode_empty_single")
+    e = F.encode(torch.zeros((0, 128), dtype=torch.float16, device="cuda"))
+    assert e.numel() == 0
+    x = rand_x(1, 64, 5)[:1]
+    b = F.encode(torch.from_numpy(x).cuda())
+    assert_same_bin(bin_from_blob(b, 1, 64), O.binary_encode(x))
+
+
+def test_online_encode_ring_slots():
+    """online_encode_token writes slot current_len % max_seq of each (b,h) and
+    nothing else (src/online_encode.cu:31-34,139)."""
+    import bitcache_amd as bc
+    say("case online_encode_ring")
+    B, H, d, max_seq = 2, 3, 128, 5
+    n = B * H * max_seq
+    kb = torch.zeros(n * 36, dtype=torch.uint8, device="cuda")
+    kr = torch.zeros(n * 130, dtype=torch.uint8, device="cuda")
+    rng = np.random.default_rng(7)
+    toks = []
+    for step in range(7):
+        x = (rng.standard_normal((B, H, d)) * 0.3).astype(np.float16)
+        toks.append(x)
+        bc._C.online_encode_token(torch.from_numpy(x).cuda(), kb, kr, B, H, d, step, max_seq)
+    got_b = bin_from_blob(kb, n, d)
+    got_r = res_from_blob(kr, n, d)
+    # slot s holds the last token written there
+    for slot in range(max_seq):
+        last = max(t for t in range(7) if t % max_seq == slot)
+        x = toks[last].reshape(B * H, d)
+        eb, er = O.online_encode(x)
+        idx = np.arange(B * H) * max_seq + slot
+        assert np.array_equal(got_b.words[idx], eb.words)
+        assert np.array_equal(got_b.scale[idx].view(np.uint16), eb.scale.view(np.uint16))
+        assert np.array_equal(got_r.codes[idx], er.codes)
+        assert np.array_equal(got_r.scale[idx].view(np.uint16), er.scale.view(np.uint16))
+    # binary-only cache: residual pointer None writes nothing else
+    kb2 = torch.zeros(n * 36, dtype=torch.uint8, device="cuda")
+    bc._C.online_encode_token(torch.from_numpy(toks[0]).cuda(), kb2, None, B, H, d, 0, max_seq)
+    torch.cuda.synchronize()
+    eb, _ = O.online_encode(toks[0].reshape(B * H, d))
+    got = bin_from_blob(kb2, n, d)
+    assert np.array_equal(got.words[np.arange(B * H) * max_seq], eb.words)
+
+
+def test_encode_into_cache_equals_appends():
+    import bitcache_amd as bc
+    say("case encode_into_cache")
+    B, H, S, d, max_seq, start = 2, 2, 37, 64, 50, 3
+    rows = B * H
+    n = rows * max_seq
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((rows, S, d)) * 0.2).astype(np.float16)
+    kb = torch.zeros(n * 36, dtype=torch.uint8, device="cuda")
+    kr = torch.zeros(n * 130, dtype=torch.uint8, device="cuda")
+    bc._C.encode_into_cache(torch.from_numpy(x).cuda(), kb, kr, rows, S, d, start, max_seq, True)
+    kb2 = torch.zeros_like(kb)
+    kr2 = torch.zeros_like(kr)
+    for s in range(S):
+        tok = torch.from_numpy(np.ascontiguousarray(x[:, s])).cuda()
+        bc._C.online_encode_token(tok, kb2, kr2, B, H, d, start + s, max_seq)
+    assert torch.equal(kb, kb2) and torch.equal(kr, kr2)
+
+
+def test_reference_layout_conversion(F):
+    from bitcache_amd import layout
+    say("case layout_conversion")
+    for d in (64, 128, 256):
+        n = 257
+        x = rand_x(n, d, 100 + d)
+        xt = torch.from_numpy(x).cuda()
+        b = F.encode(xt)
+        r = F.compute_residual(xt, b)
+        ref_b = to_np(layout.to_reference(b, d, False)).reshape(n, 36)
+        ref_r = to_np(layout.to_reference(r, d, True)).reshape(n, 130)
+        eb = O.binary_encode(x)
+        er = O.residual_encode(x, eb)
+        # reference struct: u32 words[8] (unused words zero) + fp16 scale at byte 32
+        words = np.zeros((n, 8), np.uint32)
+        words[:, : d // 32] = eb.words
+        assert np.array_equal(ref_b[:, :32].copy().view("<u4"), words)
+        assert np.array_equal(ref_b[:, 32:34].copy().view(np.float16)[:, 0].view(np.uint16),
+                              eb.scale.view(np.uint16))
+        nib = np.zeros((n, 128), np.uint8)
+        nib[:, : d // 2] = O.pack_nibbles(er.codes)
+        assert np.array_equal(ref_r[:, :128], nib)
+        assert np.array_equal(ref_r[:, 128:130].copy().view(np.float16)[:, 0].view(np.uint16),
+                              er.scale.view(np.uint16))
+        pb, pr = n * (d // 8 + 2), n * (d // 2 + 2)
+        assert torch.equal(layout.from_reference(layout.to_reference(b, d, False), d, False)[:pb], b[:pb])
+        assert torch.equal(layout.from_reference(layout.to_reference(r, d, True), d, True)[:pr], r[:pr])
+
+
+def test_encode_prefill_scale_property(F):
+    """c3-sized prefill slice: fused fp16-scale encode == two-step encode bytes
+    on 2M vectors, and a random sample of vectors matches the oracle."""
+    say("case encode_prefill_2M")
+    n, d = 2 * 1024 * 1024, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    x = (torch.randn((n, d), generator=g, device="cuda") / np.sqrt(128.0)
+         * torch.exp(0.25 * torch.randn((n, 1), generator=g, device="cuda"))).half()
+    b = F.encode(x)
+    r = F.compute_residual(x, b)
+    fb, fr = F.encode_fused(x)
+    pb, pr = n * (d // 8 + 2), n * (d // 2 + 2)
+    assert torch.equal(fb[:pb], b[:pb]) and torch.equal(fr[:pr], r[:pr])
+    idx = np.random.default_rng(0).choice(n, 4096, replace=False)
+    xs = to_np(x[torch.from_numpy(idx).cuda()])
+    eb = O.binary_encode(xs)
+    er = O.residual_encode(xs, eb)
+    gb = bin_from_blob(b, n, d)
+    gr = res_from_blob(r, n, d)
+    assert np.array_equal(gb.words[idx], eb.words)
+    assert np.array_equal(gb.scale[idx].view(np.uint16), eb.scale.view(np.uint16))
+    assert np.array_equal(gr.codes[idx], er.codes)
