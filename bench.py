@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 reference kernel")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter pass for rocprofv3 --pmc: one 1 GiB device copy (calibration) "
+                         "then --steps attention steps, no timing output")
     return ap.parse_args()
 
 
@@ -142,6 +145,19 @@ def main():
 
     def step():
         return _C.attention(q, kb, kr, vb, vr, B, H, H, S, S, d)
+
+    if args.probe:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)                  # reads and writes exactly 1 GiB
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "done", "copy_bytes": 1 << 30, "attention_steps": args.steps}))
+        return
 
     for _ in range(args.warmup):
         step()

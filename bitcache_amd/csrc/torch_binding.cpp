@@ -6,7 +6,7 @@
 // outputs (and split-KV workspaces) through PyTorch's caching allocator and
 // calls the C ABI on the current HIP stream; a non-zero status becomes a
 // RuntimeError carrying bc_last_error().
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
@@ -55,7 +55,7 @@ torch::Tensor binary_encode(torch::Tensor src) {
     const int64_t d = src.size(1);
     TORCH_CHECK(d % 32 == 0, "head_dim must be a multiple of 32");
     TORCH_CHECK(d <= 256, "head_dim exceeds MAX_HEAD_DIM=256");
-    c10::hip::HIPGuard guard(src.device());
+    c10::DeviceGuard guard(src.device());
     auto out = torch::empty({n * bc_sizeof_binary_vec()},
                             torch::TensorOptions().dtype(torch::kUInt8).device(src.device()));
     check_status(bc_binary_encode(src.data_ptr(), out.data_ptr(), n, (int)d, stream_of(src)),
@@ -73,7 +73,7 @@ torch::Tensor residual_encode(torch::Tensor src, torch::Tensor binary_blob) {
     TORCH_CHECK(d % 32 == 0, "head_dim must be a multiple of 32");
     TORCH_CHECK(d <= 256, "head_dim exceeds MAX_HEAD_DIM=256");
     TORCH_CHECK(binary_blob.numel() == n * bc_sizeof_binary_vec(), "binary_blob size mismatch");
-    c10::hip::HIPGuard guard(src.device());
+    c10::DeviceGuard guard(src.device());
     auto out = torch::empty({n * bc_sizeof_residual_vec()},
                             torch::TensorOptions().dtype(torch::kUInt8).device(src.device()));
     check_status(bc_residual_encode(src.data_ptr(), binary_blob.data_ptr(), out.data_ptr(), n,
@@ -88,7 +88,7 @@ std::tuple<torch::Tensor, torch::Tensor> encode_fused(torch::Tensor src, bool fp
     const int64_t n = src.size(0);
     const int64_t d = src.size(1);
     TORCH_CHECK(d % 32 == 0 && d <= 256, "head_dim must be a multiple of 32 and <= 256");
-    c10::hip::HIPGuard guard(src.device());
+    c10::DeviceGuard guard(src.device());
     auto opts = torch::TensorOptions().dtype(torch::kUInt8).device(src.device());
     auto bin = torch::empty({n * bc_sizeof_binary_vec()}, opts);
     auto res = torch::empty({n * bc_sizeof_residual_vec()}, opts);
@@ -119,7 +119,7 @@ void online_encode_token(torch::Tensor kv, torch::Tensor binary_cache,
         check_blob_size(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
         res = residual_cache->data_ptr();
     }
-    c10::hip::HIPGuard guard(kv.device());
+    c10::DeviceGuard guard(kv.device());
     check_status(bc_online_encode_token(kv.data_ptr(), binary_cache.data_ptr(), res, (int)batch,
                                         (int)n_heads, (int)head_dim, current_len, (int)max_seq,
                                         stream_of(kv)),
@@ -148,7 +148,7 @@ void online_encode_kv(torch::Tensor k, torch::Tensor v, torch::Tensor k_bin,
         kr = k_res->data_ptr();
         vr = v_res->data_ptr();
     }
-    c10::hip::HIPGuard guard(k.device());
+    c10::DeviceGuard guard(k.device());
     check_status(bc_online_encode_kv(k.data_ptr(), v.data_ptr(), k_bin.data_ptr(), kr,
                                      v_bin.data_ptr(), vr, (int)batch, (int)n_heads, (int)head_dim,
                                      current_len, (int)max_seq, stream_of(k)),
@@ -173,7 +173,7 @@ void encode_into_cache(torch::Tensor src, torch::Tensor binary_cache,
         check_blob_size(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
         res = residual_cache->data_ptr();
     }
-    c10::hip::HIPGuard guard(src.device());
+    c10::DeviceGuard guard(src.device());
     check_status(bc_encode_into_cache(src.data_ptr(), binary_cache.data_ptr(), res, rows, (int)seq,
                                       (int)head_dim, (int)start_pos, (int)max_seq,
                                       fp32_scale ? 1 : 0, stream_of(src)),
@@ -219,7 +219,7 @@ torch::Tensor attention(torch::Tensor Q, torch::Tensor K_bin, std::optional<torc
         kr = K_res->data_ptr();
         vr = V_res->data_ptr();
     }
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
                                              (int)seq_len, (int)head_dim, &ws_bytes),
@@ -259,7 +259,7 @@ torch::Tensor attention_partial(torch::Tensor Q, torch::Tensor K_bin,
         kr = K_res->data_ptr();
         vr = V_res->data_ptr();
     }
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
                                              (int)seq_len, (int)head_dim, &ws_bytes),
@@ -282,7 +282,7 @@ torch::Tensor attention_combine(torch::Tensor ws, int64_t batch, int64_t n_heads
                                              (int)seq_len, (int)head_dim, &need),
                  "attention_workspace_size");
     TORCH_CHECK((size_t)ws.numel() * ws.element_size() >= need, "workspace too small");
-    c10::hip::HIPGuard guard(ws.device());
+    c10::DeviceGuard guard(ws.device());
     auto out = torch::empty({batch, n_heads, head_dim},
                             torch::TensorOptions().dtype(torch::kFloat16).device(ws.device()));
     check_status(bc_attention_combine(ws.data_ptr(), out.data_ptr(), (int)batch, (int)n_heads,
@@ -323,7 +323,7 @@ std::tuple<torch::Tensor, torch::Tensor> adaptive_attention(
     check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
     check_blob_size(K_res, cap, bc_sizeof_residual_vec(), "K_res");
     check_blob_size(V_res, cap, bc_sizeof_residual_vec(), "V_res");
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_adaptive_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
                                                       (int)seq_len, (int)head_dim, &ws_bytes),
@@ -357,7 +357,7 @@ std::tuple<torch::Tensor, torch::Tensor> binary_scores(torch::Tensor Q, torch::T
                 "n_heads must be a multiple of n_kv_heads");
     TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
     check_blob_size(K_bin, batch * n_kv_heads * kv_stride, bc_sizeof_binary_vec(), "K_bin");
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     auto scores = torch::empty({batch, n_heads, seq_len}, Q.options().dtype(torch::kFloat32));
     auto pcs = torch::empty({batch, n_heads, seq_len}, Q.options().dtype(torch::kInt32));
     check_status(bc_binary_scores(Q.data_ptr(), K_bin.data_ptr(), scores.data_ptr<float>(),
@@ -374,7 +374,7 @@ torch::Tensor compute_head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t
     BC_CHECK_BLOB(K_bin);
     check_same_device(Q, K_bin, "K_bin");
     check_blob_size(K_bin, batch * n_heads * seq_len, bc_sizeof_binary_vec(), "K_bin");
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     auto ent = torch::empty({batch, n_heads}, Q.options().dtype(torch::kFloat32));
     check_status(bc_compute_head_entropy(Q.data_ptr(), K_bin.data_ptr(), ent.data_ptr<float>(),
                                          (int)batch, (int)n_heads, (int)seq_len, (int)head_dim,
@@ -387,7 +387,7 @@ torch::Tensor adaptive_select(torch::Tensor entropy, double threshold) {
     BC_CHECK_DEV(entropy);
     BC_CHECK_CONTIG(entropy);
     TORCH_CHECK(entropy.scalar_type() == torch::kFloat32, "entropy must be float32");
-    c10::hip::HIPGuard guard(entropy.device());
+    c10::DeviceGuard guard(entropy.device());
     auto modes = torch::empty(entropy.sizes(), entropy.options().dtype(torch::kUInt8));
     check_status(bc_adaptive_select(entropy.data_ptr<float>(), modes.data_ptr<uint8_t>(), 1,
                                     (int)entropy.numel(), (float)threshold, stream_of(entropy)),
@@ -406,7 +406,7 @@ torch::Tensor reference_attention(torch::Tensor Q, torch::Tensor K, torch::Tenso
     TORCH_CHECK(K.numel() == batch * n_kv_heads * seq_len * head_dim &&
                     V.numel() == K.numel(),
                 "K/V must be [batch, n_kv_heads, seq_len, head_dim]");
-    c10::hip::HIPGuard guard(Q.device());
+    c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
                                              (int)seq_len, (int)head_dim, &ws_bytes),
@@ -425,7 +425,7 @@ torch::Tensor convert(torch::Tensor blob, int64_t n, int64_t head_dim, bool resi
     BC_CHECK_BLOB(blob);
     const int64_t per = residual ? bc_sizeof_residual_vec() : bc_sizeof_binary_vec();
     TORCH_CHECK(blob.numel() == n * per, "blob must hold n * ", per, " bytes");
-    c10::hip::HIPGuard guard(blob.device());
+    c10::DeviceGuard guard(blob.device());
     auto out = to_ref ? torch::empty({n * per}, blob.options()) : torch::zeros({n * per}, blob.options());
     int st;
     if (residual)

@@ -77,7 +77,7 @@ def test_bitcache_prefill_equals_appends():
     q = torch.from_numpy((rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)).cuda()
     assert torch.equal(a.attend(q), b.attend(q))
     assert a.seq_len == b.seq_len == S
-    assert abs(a.compression_ratio - (2 * d * 2 * 2) / (2 * (36 + 130))) < 1e-9
+    assert abs(a.compression_ratio - (d * 2) / (36 + 130)) < 1e-9
 
 
 def test_bitcache_rejects_bad_inputs():

@@ -25,9 +25,10 @@ def F():
 def rand_x(n, d, seed):
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((n, d)) * rng.lognormal(0, 1.5, (n, 1))).astype(np.float16)
-    x[0] = 0.5
-    x[1, ::2] = np.float16(-0.0)
-    x[2, :3] = [np.inf, -np.inf, np.nan]
+    if n >= 3:
+        x[0] = 0.5
+        x[1, ::2] = np.float16(-0.0)
+        x[2, :3] = [np.inf, -np.inf, np.nan]
     return x
 
 
@@ -49,7 +50,8 @@ def test_encode_golden(F, d):
     got_r1 = res_from_blob(r1, n, d)
     assert np.array_equal(got_r1.codes, GOLDEN[f"enc_d{d}_codes_online"])
     assert np.array_equal(got_r1.scale.view(np.uint16), GOLDEN[f"enc_d{d}_rscale_online"])
-    assert torch.equal(b1, b)
+    pb = n * (d // 8 + 2)    # payload bytes; the rest of each blob is unused capacity
+    assert torch.equal(b1[:pb], b[:pb])
 
 
 @pytest.mark.parametrize("d", ALL_DIMS)
