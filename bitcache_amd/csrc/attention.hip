@@ -17,29 +17,17 @@
 // The workgroup folds its 4 waves into one (m, l, acc[D]) partial per query
 // head in the workspace; attn_combine_kernel merges the splits.
 #include <math.h>
+#include <stdlib.h>
 
-#include "common.h"
+#include "attn.h"
+
+using bc::AttnArgs;
+using bc::kLog2e;
+using bc::MODE_BINARY;
+using bc::MODE_COMP;
+using bc::MODE_ADAPTIVE;
 
 namespace {
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-enum AttnMode : int { MODE_BINARY = 0, MODE_COMP = 1, MODE_ADAPTIVE = 2 };
-
-struct AttnArgs {
-    const uint16_t* q;  // [B, Hq, D] fp16
-    BinPlanes kb, vb;
-    ResPlanes kr, vr;
-    int B, Hq, Hkv, S, kv_stride;
-    int n_splits, chunk;  // chunk: keys per split (multiple of 64)
-    float* ws;            // [B*Hq][n_splits][D + 2]: m (log2 domain), l, acc[D]
-    // adaptive selection (MODE_ADAPTIVE)
-    const uint32_t* thresh;      // [B*Hq] ordered key threshold
-    const int32_t* need;         // [B*Hq] ties at the threshold still to take
-    const int32_t* tie_prefix;   // [B*Hq][n_tiles] ties in earlier 64-key tiles
-    int n_tiles;
-    uint8_t* selected;           // optional [B, Hq, S]
-};
 
 template <int D>
 struct QPrep {
@@ -777,6 +765,14 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.n_tiles = (seq_len + 63) / 64;
     a.selected = selected;
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
+    // matrix-core value phase for head_dim 64/128/256; the VALU kernel covers the
+    // other head dims (and is selectable with BITCACHE_VALU_ATTENTION=1)
+    static const bool force_valu = [] {
+        const char* e = getenv("BITCACHE_VALU_ATTENTION");
+        return e != nullptr && e[0] == '1';
+    }();
+    if (!force_valu && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st))
+        return bc::check_launch("attention split (mfma)");
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }

@@ -1,0 +1,31 @@
+// Shared declarations of the split-KV attention kernels (attention.hip,
+// attention_mfma.hip).
+#pragma once
+
+#include "common.h"
+
+namespace bc {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum AttnMode : int { MODE_BINARY = 0, MODE_COMP = 1, MODE_ADAPTIVE = 2 };
+
+struct AttnArgs {
+    const uint16_t* q;  // [B, Hq, D] fp16
+    BinPlanes kb, vb;
+    ResPlanes kr, vr;
+    int B, Hq, Hkv, S, kv_stride;
+    int n_splits, chunk;  // chunk: keys per split (multiple of 64)
+    float* ws;            // [B*Hq][n_splits][D + 2]: m (log2 domain), l, acc[D]
+    // adaptive selection (MODE_ADAPTIVE)
+    const uint32_t* thresh;      // [B*Hq] ordered key threshold
+    const int32_t* need;         // [B*Hq] ties at the threshold still to take
+    const int32_t* tie_prefix;   // [B*Hq][n_tiles] ties in earlier 64-key tiles
+    int n_tiles;
+    uint8_t* selected;           // optional [B, Hq, S]
+};
+
+// MFMA value-phase kernels (attention_mfma.hip): true if (D, G, mode) is
+// handled there and the launch was issued.
+bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st);
+}  // namespace bc
