@@ -655,7 +655,14 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
     const int groups = batch * hkv * ((hq / hkv) / p.G);
     const int tiles = (S + 63) / 64;
     const int cu = bc::device_cu_count();
-    int want = (4 * cu + groups - 1) / groups;   // aim for ~4 workgroups per CU
+    // ~8 workgroups per CU: several rounds of 2-3 resident workgroups per CU keep
+    // the tail of the launch short (measured on the 64K-context MHA step)
+    int want = (8 * cu + groups - 1) / groups;
+    static const int forced = [] {
+        const char* e = getenv("BITCACHE_SPLITS");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced > 0) want = forced;
     int max_split = (tiles + 7) / 8;             // at least 8 tiles (2 per wave) per split
     if (max_split < 1) max_split = 1;
     if (want > max_split) want = max_split;

@@ -14,7 +14,9 @@
 // 64 keys) is copied global->LDS with direct loads, then ds_read_b64_tr_b4
 // transposes 16 keys x 16 nibbles per 16-lane group so that each lane holds
 // 16 keys of one dimension.  Nibbles (u) and sign bits become exact fp16
-// subnormals (value * 2^-24) with one shift + one mask per pair, and
+// subnormals (value * 2^(j-24) for bit position j < 10) with one mask per
+// pair of keys, left in place (the power of two is folded into the weights
+// of odd keys and into the accumulator of bit p), and
 // v_mfma_f32_16x16x32_f16 accumulates dims x weight-columns, where the weight
 // columns are (hi, lo) fp16 splits of a and b for each query head of the
 // group.  The fp32 accumulators are rescaled on running-max changes.
@@ -43,16 +45,31 @@ struct QDigits {
     float dq[G];                  // fixed-point step of q_int
 };
 
-// Per-wave LDS: V staging (codes then signs) and the (hi, lo) fp16 weight
-// columns; the epilogue reuses it for [2 parts][G][D] partial sums + G offsets.
+// Per-wave LDS: two V staging buffers (tile i is consumed while tile i+1
+// lands), each the tile's code bytes then its sign bytes, then the (hi, lo)
+// fp16 weight columns [part][2G][64 slots].  The epilogue
+// reuses the region for [2 parts][G][D] partial sums + G offsets.
 template <int D, int G>
 struct WaveLds {
     static constexpr int kCodeBytes = 64 * D / 2;
-    static constexpr int kSignBytes = 64 * D / 8;
-    static constexpr int kWeightBytes = 2 * 16 * 64 * 2;  // [part][col][slot] fp16
-    static constexpr int kMain = kCodeBytes + kSignBytes + kWeightBytes;
+    // D = 64: 8-byte sign rows are copied two keys per lane by all 64 lanes
+    // (lanes 32..63 repeat lanes 0..31 into the second half), hence 1 KB
+    static constexpr int kSignBytes = 64 * D / 8 > 1024 ? 64 * D / 8 : 1024;
+    static constexpr int kStage = kCodeBytes + kSignBytes;
+    static constexpr int kWeightBytes = 2 * 2 * G * 64 * 2;
+    static constexpr int kMain = 2 * kStage + kWeightBytes;
     static constexpr int kEpi = ((2 * G * D + G) * 4 + 15) / 16 * 16;
     static constexpr int kBytes = kMain > kEpi ? kMain : kEpi;
+};
+
+// K-side data of one 64-key tile held in registers: sign words and scales of
+// the lane's own key, and the lane's code pieces (see the kernel).
+template <int D>
+struct KRegs {
+    SignWords<D> ks;
+    uint32_t kc[D / 8];
+    uint16_t sk, svv, rsk, rsv;   // raw fp16 scales (converted at use, so the
+                                  // loads of the next tile are not waited on)
 };
 
 __device__ __forceinline__ uint16_t f2h_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
@@ -105,10 +122,28 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 
 // Resident waves per SIMD the register allocation targets: two for small
 // query groups (memory latency is hidden by the second wave), one otherwise.
+#ifndef BC_MHA_WAVES
+#define BC_MHA_WAVES 3
+#endif
+#ifndef BC_LIN_K
+#define BC_LIN_K 0
+#endif
+#ifndef BC_LIN_V
+#define BC_LIN_V 1
+#endif
 template <int D, int G>
 struct Occupancy {
-    static constexpr int kWaves = (G <= 2 && D <= 128) ? 2 : 1;
+    static constexpr int kWaves = (G == 1 && D <= 128) ? BC_MHA_WAVES : ((G <= 2 && D <= 128) ? 2 : 1);
 };
+
+// Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
+template <int Q>
+__device__ __forceinline__ int row_group_sum(int v) {
+    if constexpr (Q >= 2) v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+    if constexpr (Q >= 4) v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+    if constexpr (Q >= 8) v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+    return v;
+}
 
 template <int D, int G, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<D, G>::kWaves)))
@@ -118,6 +153,25 @@ void attn_mfma_kernel(AttnArgs a) {
     constexpr int CW = D / 8;    // code dwords per key
     constexpr bool RES = MODE != MODE_BINARY;
     constexpr int SB = D / 8;    // sign bytes per key
+    constexpr int CB = D / 2;    // code bytes per key
+    // Code loads.  Per key (lane = key): lane l reads its key's row in 16-byte
+    // pieces, so one load touches 64 rows.  Linear: load round i, lane l takes
+    // the 16 bytes at i*1024 + 16*l of the tile (contiguous KiB), i.e. piece
+    // l%Q of key i*(64/Q) + l/Q; for K this needs a Q-lane reduction of the
+    // partial dots.  The adaptive mode gathers only selected keys' codes and
+    // always works per key.
+    constexpr bool LIN_K = (BC_LIN_K || G > 1) && MODE == MODE_COMP;
+    constexpr bool LIN_V = BC_LIN_V && MODE == MODE_COMP;
+    constexpr int Q = D / 32;    // 16-byte pieces per code row
+    // Vector-memory operations issued per prefetched tile, counted at their
+    // fewest (a load moves at most 16 bytes; planes are separate loads), so
+    // waiting down to this many outstanding operations completes everything
+    // issued before the prefetch and never less.
+    constexpr int kSignDma = SB >= 16 ? SB / 16 : 1;
+    constexpr int kVDma = kSignDma + (MODE == MODE_COMP ? Q : 0);
+    constexpr int kKLoads = (SB + 15) / 16 + (MODE == MODE_COMP ? 4 + Q : 2);
+    constexpr int kPrefetchOps = kVDma + kKLoads;
+    static_assert(kPrefetchOps + kVDma < 64, "vmcnt holds 6 bits");
     using WL = WaveLds<D, G>;
 
     __shared__ QDigits<D, G> qd;
@@ -135,17 +189,20 @@ void attn_mfma_kernel(AttnArgs a) {
 
     prep_digits<D, G>(a.q + (int64_t)bhq0 * D, qd, qf);
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index is uniform: readfirstlane lets the compiler keep the tile
+    // loop in scalar registers (a uniform loop, not an exec-masked one)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g4 = lane >> 4, lj = lane & 15;
     const int key_begin = split * a.chunk;
     const int key_end = min(a.S, key_begin + a.chunk);
     const int64_t kv_base = (int64_t)bkv * a.kv_stride;
     const float isd2 = (1.0f / sqrtf((float)D)) * kLog2e;
+    // the key whose score this lane computes (tile-relative)
+    const int kown = LIN_K ? (lane % Q) * (64 / Q) + lane / Q : lane;
+    const int quarter = lane % Q;
 
     uint8_t* my = wave_lds[wave];
-    uint8_t* st_codes = my;                              // [D/32 chunks][64 keys][16 B]
-    uint8_t* st_signs = my + WL::kCodeBytes;             // SB >= 16: [SB/16][64][16 B]; SB == 8: [64][8 B]
-    uint16_t* wts = (uint16_t*)(my + WL::kCodeBytes + WL::kSignBytes);  // [2][16][64]
+    uint16_t* wts = (uint16_t*)(my + 2 * WL::kStage);  // [2 parts][2G cols][64 slots]
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
@@ -183,10 +240,10 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // query digits: one head -> scalar registers for the whole loop (uniform
-    // operands of v_dot8); several heads -> re-read from LDS every tile
-    int sdig[G == 1 ? CW : 1][4];
-    if constexpr (G == 1) {
+    // query digits of a single head in scalar registers for the whole loop
+    // (uniform operands of v_dot8) when codes are read per key
+    int sdig[(G == 1 && MODE == MODE_COMP && !LIN_K) ? CW : 1][4];
+    if constexpr (G == 1 && MODE == MODE_COMP && !LIN_K) {
 #pragma unroll
         for (int w = 0; w < CW; w++) {
             const int4 dg = qd.digits[0][w];
@@ -197,57 +254,92 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     }
 
-    for (int t0 = key_begin + wave * 64; t0 < key_end; t0 += 4 * 64) {
-        const int s = t0 + lane;
+    // byte offset of the 16-byte piece `off` of a tile row plane with `rb`
+    // bytes per key; pieces of keys past the range re-read key t0's row (in
+    // range; their weight is 0), so every lane issues the same loads and no
+    // branch surrounds a load (the compiler's wait counts stay exact)
+    auto piece = [&](int t0, int off_in_tile, int rb) -> int64_t {
+        const int k = t0 + off_in_tile / rb;
+        return k < key_end ? (kv_base + t0) * rb + off_in_tile : (kv_base + t0) * rb + off_in_tile % rb;
+    };
+
+    // ---------------- loads of one tile: K side into registers, V side to LDS
+    auto load_k = [&](KRegs<D>& r, int t0) {
+        const int s = t0 + kown;
+        const int64_t ki = kv_base + (s < key_end ? s : t0);
+        r.ks = load_signs<D>(a.kb.signs + ki * SB);
+        r.sk = a.kb.scales[ki];
+        r.svv = a.vb.scales[ki];
+        r.rsk = 0;
+        r.rsv = 0;
+        if constexpr (MODE == MODE_COMP) {
+            r.rsk = a.kr.scales[ki];
+            r.rsv = a.vr.scales[ki];
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                const uint4 c = *(const uint4*)(a.kr.codes + (LIN_K ? piece(t0, i * 1024 + 16 * lane, CB)
+                                                                    : ki * CB + 16 * i));
+                r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+            }
+        }
+    };
+    // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear)
+    // or piece c at c*1024 + 16k (per key)
+    auto issue_v = [&](int buf, int t0) {
+        uint8_t* st_codes = my + buf * WL::kStage;
+        uint8_t* st_signs = st_codes + WL::kCodeBytes;
+        if constexpr (SB >= 16) {
+#pragma unroll
+            for (int c = 0; c < SB / 16; c++)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void*)(a.vb.signs + piece(t0, c * 1024 + 16 * lane, SB)),
+                    LDS_PTR(void, st_signs + c * 1024), 16, 0, 0);
+        } else {
+            // 8-byte rows: one KiB load covers 128 rows, so lanes 32..63 repeat
+            // lanes 0..31 (into bytes 512..1023).  The second key of the blob's
+            // last pair reads the first 8 bytes of the scale plane that follows
+            // the signs (the host guarantees 4 entries), and gets weight 0.
+            const int k2 = t0 + 2 * (lane & 31);
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void*)(a.vb.signs +
+                                                                (kv_base + (k2 < key_end ? k2 : t0)) * SB),
+                LDS_PTR(void, st_signs), 16, 0, 0);
+        }
+        if constexpr (MODE == MODE_COMP) {
+            const int s = t0 + lane;
+            const int64_t ki = kv_base + (s < key_end ? s : t0);
+#pragma unroll
+            for (int c = 0; c < Q; c++)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void*)(a.vr.codes + (LIN_V ? piece(t0, c * 1024 + 16 * lane, CB)
+                                                                                         : ki * CB + 16 * c)),
+                    LDS_PTR(void, st_codes + c * 1024), 16, 0, 0);
+        }
+    };
+
+    // ---------------- one tile: scores, online softmax, value MFMAs
+    auto process = [&](const KRegs<D>& r, int t0, int buf) {
+        uint8_t* st_codes = my + buf * WL::kStage;
+        uint8_t* st_signs = st_codes + WL::kCodeBytes;
+        const int s = t0 + kown;
         const bool valid = s < key_end;
         const int64_t ki = kv_base + (valid ? s : t0);
-
-        // ---------------- V tile: global -> LDS
-        if constexpr (SB >= 16) {
-            if (valid) {  // lane = key: 16-byte chunks land at chunk*1024 + 16*lane
-                const uint8_t* vs = a.vb.signs + ki * SB;
-#pragma unroll
-                for (int c = 0; c < SB / 16; c++)
-                    __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void*)(vs + 16 * c),
-                        LDS_PTR(void, st_signs + c * 1024), 16, 0, 0);
-            }
-        } else {
-            // 8-byte sign rows: lane l < 32 copies keys 2l and 2l+1 (16 bytes; a
-            // second key past the range reads the blob's own next bytes and gets
-            // weight 0)
-            if (lane < 32 && t0 + 2 * lane < key_end)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(a.vb.signs +
-                                                                    (kv_base + t0 + 2 * lane) * SB),
-                    LDS_PTR(void, st_signs), 16, 0, 0);
+        // this tile's K registers: the younger operations are this tile's V
+        // loads and the whole next-tile prefetch.  An explicit count keeps the
+        // compiler from draining the queue (with direct-to-LDS loads pending it
+        // would wait for zero).
+        if constexpr (MODE != MODE_ADAPTIVE) {
+            constexpr int n = kVDma + kPrefetchOps;
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (MODE == MODE_COMP) {
-            if (valid) {
-                const uint8_t* vc = a.vr.codes + ki * (D / 2);
-#pragma unroll
-                for (int c = 0; c < D / 32; c++)
-                    __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void*)(vc + 16 * c),
-                        LDS_PTR(void, st_codes + c * 1024), 16, 0, 0);
-            }
-        }
-
-        // ---------------- score phase (lane = key)
-        const SignWords<D> ks = load_signs<D>(a.kb.signs + ki * (D / 8));
-        const float sk = h2f(a.kb.scales[ki]);
-        const float svv = h2f(a.vb.scales[ki]);
-        float rsk = 0.0f, rsv = 0.0f;
+        const float sk = h2f(r.sk), svv = h2f(r.svv);
+        float rsk = h2f(r.rsk), rsv = h2f(r.rsv);
         uint32_t kc[CW];
         if constexpr (MODE == MODE_COMP) {
-            rsk = h2f(a.kr.scales[ki]);
-            rsv = h2f(a.vr.scales[ki]);
-            const uint4* cp = (const uint4*)(a.kr.codes + ki * (D / 2));
 #pragma unroll
-            for (int i = 0; i < CW / 4; i++) {
-                const uint4 c = cp[i];
-                kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
-            }
+            for (int w = 0; w < CW; w++) kc[w] = r.kc[w];
         }
 
         float xd[G];
@@ -256,7 +348,7 @@ void attn_mfma_kernel(AttnArgs a) {
         for (int g = 0; g < G; g++) {
             int pc = 0;
 #pragma unroll
-            for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qd.signs[g][w] ^ ks.w[w]));
+            for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qd.signs[g][w] ^ r.ks.w[w]));
             const float mq = (float)(2 * pc - D);
             xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:179)
             if constexpr (MODE == MODE_ADAPTIVE) {
@@ -274,15 +366,15 @@ void attn_mfma_kernel(AttnArgs a) {
             if (selmask) {
                 rsk = h2f(a.kr.scales[ki]);
                 rsv = h2f(a.vr.scales[ki]);
-                const uint4* cp = (const uint4*)(a.kr.codes + ki * (D / 2));
+                const uint4* cp = (const uint4*)(a.kr.codes + ki * CB);
 #pragma unroll
                 for (int i = 0; i < CW / 4; i++) {
                     const uint4 c = cp[i];
                     kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
                 }
-                const uint8_t* vc = a.vr.codes + ki * (D / 2);
+                const uint8_t* vc = a.vr.codes + ki * CB;
 #pragma unroll
-                for (int c = 0; c < D / 32; c++)
+                for (int c = 0; c < Q; c++)
                     __builtin_amdgcn_global_load_lds(
                         (const __attribute__((address_space(1))) void*)(vc + 16 * c),
                         LDS_PTR(void, st_codes + c * 1024), 16, 0, 0);
@@ -298,46 +390,67 @@ void attn_mfma_kernel(AttnArgs a) {
         int racc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) racc[g] = 0;
-        if constexpr (RES) {
+        if constexpr (LIN_K) {
+            // round i: this lane holds 32 dims (quarter) of key i*(64/Q) + l/Q;
+            // partial dots are summed over the Q lanes of the row, and the lane
+            // whose own key it is keeps the total
+            int z;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(z));  // keeps digit reads per tile (not hoisted)
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int4 dg = qd.digits[g][4 * quarter + j + z];
+                        const int x = (int)kc[4 * i + j];
+                        s0 = __builtin_amdgcn_sdot8(dg.x, x, s0, false);
+                        s1 = __builtin_amdgcn_sdot8(dg.y, x, s1, false);
+                        s2 = __builtin_amdgcn_sdot8(dg.z, x, s2, false);
+                        s3 = __builtin_amdgcn_sdot8(dg.w, x, s3, false);
+                    }
+                    const int tot = row_group_sum<Q>(s0 + 16 * s1 + 256 * s2 + 4096 * s3);
+                    racc[g] = quarter == i ? tot : racc[g];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else if constexpr (G == 1 && MODE == MODE_COMP) {
+            {
+                int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+                for (int w = 0; w < CW; w++) {
+                    s0 = __builtin_amdgcn_sdot8(sdig[w][0], (int)kc[w], s0, false);
+                    s1 = __builtin_amdgcn_sdot8(sdig[w][1], (int)kc[w], s1, false);
+                    s2 = __builtin_amdgcn_sdot8(sdig[w][2], (int)kc[w], s2, false);
+                    s3 = __builtin_amdgcn_sdot8(sdig[w][3], (int)kc[w], s3, false);
+                }
+                racc[0] = s0 + 16 * s1 + 256 * s2 + 4096 * s3;
+            }
+        } else if constexpr (RES) {
             bool any_res = MODE == MODE_COMP;
             if constexpr (MODE == MODE_ADAPTIVE) any_res = selmask != 0u;
             if (any_res) {
-                if constexpr (G == 1) {
-                    int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+                int sa[G][4];
 #pragma unroll
-                    for (int w = 0; w < CW; w++) {
-                        s0 = __builtin_amdgcn_sdot8(sdig[w][0], (int)kc[w], s0, false);
-                        s1 = __builtin_amdgcn_sdot8(sdig[w][1], (int)kc[w], s1, false);
-                        s2 = __builtin_amdgcn_sdot8(sdig[w][2], (int)kc[w], s2, false);
-                        s3 = __builtin_amdgcn_sdot8(sdig[w][3], (int)kc[w], s3, false);
+                for (int g = 0; g < G; g++) sa[g][0] = sa[g][1] = sa[g][2] = sa[g][3] = 0;
+                int z;
+                asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+#pragma unroll
+                for (int w = 0; w < CW; w++) {
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const int4 dg = qd.digits[g][w + z];
+                        sa[g][0] = __builtin_amdgcn_sdot8(dg.x, (int)kc[w], sa[g][0], false);
+                        sa[g][1] = __builtin_amdgcn_sdot8(dg.y, (int)kc[w], sa[g][1], false);
+                        sa[g][2] = __builtin_amdgcn_sdot8(dg.z, (int)kc[w], sa[g][2], false);
+                        sa[g][3] = __builtin_amdgcn_sdot8(dg.w, (int)kc[w], sa[g][3], false);
                     }
-                    racc[0] = s0 + 16 * s1 + 256 * s2 + 4096 * s3;
-                } else {
-                    int sa[G][4];
-#pragma unroll
-                    for (int g = 0; g < G; g++) sa[g][0] = sa[g][1] = sa[g][2] = sa[g][3] = 0;
-                    // an opaque zero makes the digit reads loop-variant, so they are
-                    // not hoisted out of the tile loop (64 registers per head)
-                    int z;
-                    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-                    // code dword outer, head inner: each head's digit quad is one
-                    // 16-byte LDS read right before its four v_dot8
-#pragma unroll
-                    for (int w = 0; w < CW; w++) {
-#pragma unroll
-                        for (int g = 0; g < G; g++) {
-                            const int4 dg = qd.digits[g][w + z];
-                            sa[g][0] = __builtin_amdgcn_sdot8(dg.x, (int)kc[w], sa[g][0], false);
-                            sa[g][1] = __builtin_amdgcn_sdot8(dg.y, (int)kc[w], sa[g][1], false);
-                            sa[g][2] = __builtin_amdgcn_sdot8(dg.z, (int)kc[w], sa[g][2], false);
-                            sa[g][3] = __builtin_amdgcn_sdot8(dg.w, (int)kc[w], sa[g][3], false);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-#pragma unroll
-                    for (int g = 0; g < G; g++)
-                        racc[g] = sa[g][0] + 16 * sa[g][1] + 256 * sa[g][2] + 4096 * sa[g][3];
+                    __builtin_amdgcn_sched_barrier(0);
                 }
+#pragma unroll
+                for (int g = 0; g < G; g++)
+                    racc[g] = sa[g][0] + 16 * sa[g][1] + 256 * sa[g][2] + 4096 * sa[g][3];
             }
         }
         float sc[G];
@@ -350,7 +463,7 @@ void attn_mfma_kernel(AttnArgs a) {
             sc[g] = valid ? score * isd2 : -INFINITY;
         }
 
-        // ---------------- weight scale for this tile (p <= 1, so w <= max(2 sv, rs/7))
+        // weight scale for this tile (p <= 1, so w <= max(2 sv, rs/7))
         {
             float wb = valid ? fmaxf(2.0f * svv, rsv * (1.0f / 7.0f)) : 0.0f;
             wb = wave_max(wb);
@@ -375,9 +488,14 @@ void attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        // ---------------- online softmax, weights for the value MFMAs
+        // online softmax; (hi, lo) fp16 weights to LDS in MFMA slot order
         float lane_alpha = 1.0f;
         bool any_rescale = false;
+        const int sl = slot_of(kown);
+        // the value operands of odd keys come out 16x larger (see the MFMA
+        // loops below): their weights carry 1/16 so that every product is exact
+        const float kfac = (kown & 1) ? 0.0625f : 1.0f;
+        const float kinv = (kown & 1) ? 16.0f : 1.0f;
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float mt = wave_max(sc[g]);
@@ -392,22 +510,23 @@ void attn_mfma_kernel(AttnArgs a) {
             }
             const float p = valid ? exp2f(sc[g] - mn) : 0.0f;
             lsum[g] += p;
-            const float a2 = ldexpf(2.0f * p * svv, wexp);
+            const float a2 = ldexpf(2.0f * p * svv * kfac, wexp);
             float bv = 0.0f;
-            if constexpr (MODE == MODE_COMP) bv = ldexpf(p * (rsv * (1.0f / 7.0f)), wexp);
+            if constexpr (MODE == MODE_COMP) bv = ldexpf(p * (rsv * (1.0f / 7.0f)) * kfac, wexp);
             if constexpr (MODE == MODE_ADAPTIVE)
-                bv = ((selmask >> g) & 1u) ? ldexpf(p * (rsv * (1.0f / 7.0f)), wexp) : 0.0f;
+                bv = ((selmask >> g) & 1u) ? ldexpf(p * (rsv * (1.0f / 7.0f)) * kfac, wexp) : 0.0f;
             const uint16_t a2h = f2h_bits(a2);
             const uint16_t a2l = f2h_bits(a2 - h_bits2f(a2h));
             const uint16_t bh = f2h_bits(bv);
             const uint16_t bl = f2h_bits(bv - h_bits2f(bh));
             // offset removed at the end: sum_s (a_s + 8 b_s) with the weights as rounded
-            off[g] += 0.5f * (h_bits2f(a2h) + h_bits2f(a2l)) + 8.0f * (h_bits2f(bh) + h_bits2f(bl));
-            const int sl = slot_of(lane);
-            wts[(0 * 16 + 2 * g) * 64 + sl] = a2h;
-            wts[(0 * 16 + 2 * g + 1) * 64 + sl] = a2l;
-            wts[(1 * 16 + 2 * g) * 64 + sl] = bh;
-            wts[(1 * 16 + 2 * g + 1) * 64 + sl] = bl;
+            off[g] += kinv * (0.5f * (h_bits2f(a2h) + h_bits2f(a2l)) + 8.0f * (h_bits2f(bh) + h_bits2f(bl)));
+            wts[(0 * 2 * G + 2 * g) * 64 + sl] = a2h;
+            wts[(0 * 2 * G + 2 * g + 1) * 64 + sl] = a2l;
+            if constexpr (RES) {
+                wts[(1 * 2 * G + 2 * g) * 64 + sl] = bh;
+                wts[(1 * 2 * G + 2 * g + 1) * 64 + sl] = bl;
+            }
         }
         if (any_rescale) {
             if (my_head >= G) lane_alpha = 1.0f;
@@ -419,8 +538,16 @@ void attn_mfma_kernel(AttnArgs a) {
             for (int d = 0; d < NB; d++) cn[d] *= lane_alpha;
         }
 
-        // V tile and weights must be in LDS before the transposed reads
-        __builtin_amdgcn_s_waitcnt(0);
+        // this tile's V data must be in LDS: everything but the next tile's
+        // loads (the youngest kPrefetchOps vector-memory operations) completes
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MODE != MODE_ADAPTIVE) {
+            constexpr int n = kPrefetchOps;
+            __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the weight stores above
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
@@ -429,29 +556,35 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int mh = 0; mh < 2; mh++) {
             if (my_col < 2 * G) {
-                bsig[mh] = *(const h8_t*)&wts[(0 * 16 + my_col) * 64 + 16 * g4 + 8 * mh];
-                bres[mh] = *(const h8_t*)&wts[(1 * 16 + my_col) * 64 + 16 * g4 + 8 * mh];
+                bsig[mh] = *(const h8_t*)&wts[(0 * 2 * G + my_col) * 64 + 16 * g4 + 8 * mh];
+                if constexpr (RES) bres[mh] = *(const h8_t*)&wts[(1 * 2 * G + my_col) * 64 + 16 * g4 + 8 * mh];
+                else bres[mh] = bsig[mh];
             } else {
                 bsig[mh] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
                 bres[mh] = bsig[mh];
             }
         }
 
-        // ---------------- sign part: rows = dims 64h + 4*lj + p
+        // sign part: rows = dims 64h + 4*lj + p
         const int row_key = 16 * g4 + lj;  // this lane addresses row (key) lj of its group
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            const uint8_t* rp = (SB >= 16) ? st_signs + (h >> 1) * 1024 + 16 * row_key + 8 * (h & 1)
-                                           : st_signs + 8 * row_key;
+            const uint8_t* rp = st_signs + SB * row_key + 8 * h;
             const v2i_t w = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
 #pragma unroll
             for (int mh = 0; mh < 2; mh++) {
+                // x holds nibble r of key r (r = 0..3) and of key r + 4 (bits
+                // 16 + 4r): pair word k keeps bit p of keys k and k + 4 in place,
+                // an fp16 subnormal 2^(4(k&1) + p - 24); keys 2, 3 via x >> 8
                 const uint32_t x = (uint32_t)(mh ? w.y : w.x);
+                const uint32_t y = x >> 8;
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     uint32_t pw[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) pw[k] = (x >> (4 * k + p)) & 0x00010001u;
+                    pw[0] = x & (0x00010001u << p);
+                    pw[1] = x & (0x00100010u << p);
+                    pw[2] = y & (0x00010001u << p);
+                    pw[3] = y & (0x00100010u << p);
                     const h8_t av = __builtin_bit_cast(h8_t, pw);
                     cs[h][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bsig[mh], cs[h][p], 0, 0, 0);
                 }
@@ -459,21 +592,26 @@ void attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        // ---------------- residual part: rows = dims 16db + lj
+        // residual part: rows = dims 16db + lj
         if constexpr (RES) {
             bool any_sel = true;
             if constexpr (MODE == MODE_ADAPTIVE) any_sel = __ballot(selmask != 0u) != 0ull;
             if (any_sel) {
 #pragma unroll
                 for (int db = 0; db < NB; db++) {
-                    const uint8_t* rp = st_codes + (db >> 1) * 1024 + 16 * row_key + 8 * (db & 1);
+                    const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 8 * db
+                                            : st_codes + (db >> 1) * 1024 + 16 * row_key + 8 * (db & 1);
                     const v2i_t w = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
 #pragma unroll
                     for (int mh = 0; mh < 2; mh++) {
+                        // u = n + 8 in place: keys k, k + 4 at 4(k&1) (odd keys 16x)
                         const uint32_t x = (uint32_t)(mh ? w.y : w.x) ^ 0x88888888u;
+                        const uint32_t y = x >> 8;
                         uint32_t pw[4];
-#pragma unroll
-                        for (int k = 0; k < 4; k++) pw[k] = (x >> (4 * k)) & 0x000F000Fu;
+                        pw[0] = x & 0x000F000Fu;
+                        pw[1] = x & 0x00F000F0u;
+                        pw[2] = y & 0x000F000Fu;
+                        pw[3] = y & 0x00F000F0u;
                         const h8_t av = __builtin_bit_cast(h8_t, pw);
                         cn[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bres[mh], cn[db], 0, 0, 0);
                     }
@@ -481,7 +619,38 @@ void attn_mfma_kernel(AttnArgs a) {
                 }
             }
         }
-        // all LDS reads of this tile retire before the next tile's loads land
+        // the staging buffer is refilled two tiles later: its reads retire here
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    // ---------------- software-pipelined tile loop: tile i+1 loads in flight
+    // while tile i computes (two register sets, two LDS staging buffers).  The
+    // prefetch after a wave's last tile re-reads that tile (harmless, cached)
+    // so that no load sits behind a branch.
+    int t = key_begin + wave * 64;
+    if (t < key_end) {
+        KRegs<D> ka, kb;
+        load_k(ka, t);
+        issue_v(0, t);
+        int tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+        load_k(kb, tp);
+        issue_v(1, tp);
+        for (;;) {
+            process(ka, t, 0);
+            t += 4 * 64;
+            if (t >= key_end) break;
+            tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+            load_k(ka, tp);
+            issue_v(0, tp);
+            process(kb, t, 1);
+            t += 4 * 64;
+            if (t >= key_end) break;
+            tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+            load_k(kb, tp);
+            issue_v(1, tp);
+        }
+        // the last prefetch still writes LDS that the epilogue reuses
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
     }
@@ -507,7 +676,8 @@ void attn_mfma_kernel(AttnArgs a) {
         for (int p = 0; p < 4; p++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float v = cs[h][p][i] + __shfl_xor(cs[h][p][i], 1, 64);
+                // accumulator p carries 2^p (bit p read in place)
+                const float v = (cs[h][p][i] + __shfl_xor(cs[h][p][i], 1, 64)) * (1.0f / (float)(1 << p));
                 if (my_col < 2 * G && (my_col & 1) == 0) {
                     const int dim = 64 * h + 4 * (4 * g4 + i) + p;
                     accw[(0 * G + my_head) * D + dim] = v;
@@ -577,6 +747,9 @@ void launch_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
 namespace bc {
 
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
+    // D = 64 copies sign rows in key pairs, reading up to 8 bytes past the last
+    // key's row into the scale plane: that plane holds 8 bytes from 4 entries
+    if (D == 64 && (int64_t)a.B * a.Hkv * a.kv_stride < 4) return false;
     switch (D) {
         case 64: launch_d<64>(mode, G, a, grid, st); return true;
         case 128: launch_d<128>(mode, G, a, grid, st); return true;
