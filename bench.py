@@ -46,7 +46,7 @@ def traffic_from_profiles():
     """HBM bytes per launch of the split kernel from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
     or None if no summary is present."""
-    path = os.path.join(ROOT, "profiles", "attn_split_c3_pmc.md")
+    path = os.path.join(ROOT, "profiles", "attn_mfma_kernel_c3_counters.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
@@ -168,7 +168,8 @@ def main():
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
 
-    # split kernel alone, HIP events on the current stream (the one it runs on)
+    # split kernel alone (attention_partial launches only attn_mfma_kernel), HIP
+    # events on the current stream, which is the stream the kernel runs on
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
     for i in range(args.steps):
@@ -217,7 +218,7 @@ def main():
                    "bytes_per_step": alg_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": traffic, "kernel": "attn_split_kernel<128,1,COMP>",
+                     "traffic": traffic, "kernel": "attn_mfma_kernel<128,1,COMP>",
                      "kernel_us": round(split_ms * 1e3, 1)},
         "fp16_reference": fp16,
         "speedup_vs_fp16": (round(fp16["us_per_step"] / (wall * 1e6), 3) if fp16 else None),
