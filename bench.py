@@ -12,6 +12,8 @@ the stream it runs on; cpu_baseline = the CPU oracle (PyTorch-CPU
 restatement) on a bounded sample of the same heads, extrapolated to a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fp16]
+       python bench.py --config c2|c4|c5   (one line for another workload; the
+       headline and the driver's line is the default c3)
 """
 from __future__ import annotations
 
@@ -36,6 +38,8 @@ def parse():
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 reference kernel")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
+                    help="workload (default c3, the headline)")
     ap.add_argument("--probe", action="store_true",
                     help="counter pass for rocprofv3 --pmc: one 1 GiB device copy (calibration) "
                          "then --steps attention steps, no timing output")
@@ -113,6 +117,166 @@ def cpu_baseline(q, kb, kr, vb, vr, B, H, S, d, budget_s):
     }
 
 
+def timed(fn, steps, warmup, torch):
+    """Wall-clock seconds per call of fn (device-synchronised on both sides)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def event_ms(fn, steps, torch):
+    """Median per-call milliseconds from HIP events on the current stream."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sorted(a.elapsed_time(b) for a, b in ev)[len(ev) // 2]
+
+
+def bench_c2(args, torch, _C, W):
+    """Binary-only scoring + attention, B8 H32 d128 S32768 (rotating 3 cache
+    copies: one copy is 302 MB, about the size of the 256 MB last-level cache)."""
+    cfg = W.CONFIGS["c2"]
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, _ = W.make_c2(cfg)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    copies = []
+    for i in range(3):
+        kk = k if i == 0 else (k.float() * -1.0 if i == 1 else k.float() * 0.5).half()
+        kb = _C.binary_encode(kk.view(-1, d))
+        vb = _C.binary_encode((torch.randn(kk.shape, generator=g, device="cuda") / 11.3).half().view(-1, d))
+        copies.append((kb, vb))
+    del k
+    torch.cuda.synchronize()
+    it = [0]
+
+    def attn():
+        kb, vb = copies[it[0] % 3]
+        it[0] += 1
+        return _C.binary_attention(q, kb, vb, B, H, S, d)
+
+    def scores():
+        kb, _ = copies[it[0] % 3]
+        it[0] += 1
+        return _C.binary_scores(q, kb, B, H, H, S, S, d)
+
+    wall = timed(attn, args.steps, args.warmup, torch)
+    ms_scores = event_ms(scores, args.steps, torch)
+    alg = 2 * B * H * S * W.algorithmic_bytes_per_key(d, residual=False)
+    return {
+        "metric": "binary decode-attn µs/step + achieved HBM GB/s, 32K ctx, 32 heads, d=128, batch 8",
+        "value": round(alg / wall / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4),
+        "us_per_step": round(wall * 1e6, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c2: binary-only attention (sign bits + scale), 3 rotating cache copies",
+                   "batch": B, "heads": H, "seq_len": S, "head_dim": d, "bytes_per_step": alg},
+        "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "kernel": "attention step (split + combine), wall clock"},
+        "binary_scores_us": round(ms_scores * 1e3, 1),
+        "binary_scores_gbps": round((B * H * S * (d // 8 + 2) + 8 * B * H * S) / (ms_scores * 1e-3) / 1e9, 1),
+    }
+
+
+def bench_c4(args, torch, _C, W, bitcache_amd):
+    """Online encode + decode loop: B4, GQA 32/8, prefill 16384 tokens, then
+    256 steps of (append one K/V token per kv head, attend).  tokens/s over the
+    loop; the prefill is outside the timed region."""
+    cfg = W.CONFIGS["c4"]
+    B, Hq, Hkv, S, d = cfg.batch, cfg.n_heads, cfg.n_kv_heads, cfg.seq_len, cfg.head_dim
+    T = W.C4_DECODE_STEPS
+    q0, k, v = W.make_qkv(cfg)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg.seed + 100)
+    qs = (torch.randn((T, B, Hq, d), generator=g, device="cuda") * W.SIGMA).half()
+    ks = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
+    vs = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
+    cache = bitcache_amd.BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
+
+    def loop():
+        cache.reset()
+        cache.prefill(k, v)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(T):
+            cache.append(ks[t], vs[t])
+            cache.attend(qs[t])
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    loop()  # warmup
+    runs = sorted(loop() for _ in range(3))
+    el = runs[1]
+    per_key = 2 * W.algorithmic_bytes_per_key(d)
+    alg = sum(B * Hkv * (S + t + 1) * per_key for t in range(T))
+    return {
+        "metric": "online encode + decode loop tokens/s, GQA 32/8, 16K prefill + 256 steps, d=128, batch 4",
+        "value": round(B * T / el, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": T, "warmup": T, "ms_per_step": round(el / T * 1e3, 4),
+        "us_per_step": round(el / T * 1e6, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c4: BitCache append (online_encode_kv) + attend per step, median of 3 loops",
+                   "batch": B, "heads": Hq, "kv_heads": Hkv, "prefill": S, "decode_steps": T,
+                   "head_dim": d, "cache_bytes_per_step_avg": alg // T},
+        "roofline": {"bound": "hbm", "achieved": round(alg / el / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(alg / el / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "whole step incl. host launch overhead (cache is last-level-cache resident)"},
+    }
+
+
+def bench_c5(args, torch, _C, W):
+    """Adaptive precision at long context: B16 GQA 32/8 S131072, top 10% of keys
+    per (b, query head) by binary score get the residual correction."""
+    import bitcache_amd
+    cfg = W.CONFIGS["c5"]
+    B, Hq, Hkv, S, d = cfg.batch, cfg.n_heads, cfg.n_kv_heads, cfg.seq_len, cfg.head_dim
+    q, k, v = W.make_qkv(cfg)
+    kb, kr = _C.encode_fused(k.view(-1, d), False)
+    del k
+    vb, vr = _C.encode_fused(v.view(-1, d), False)
+    del v
+    torch.cuda.synchronize()
+    top_k = bitcache_amd.default_top_k(S)
+
+    def step():
+        return _C.adaptive_attention(q, kb, kr, vb, vr, B, Hq, Hkv, S, S, d, top_k, False)
+
+    wall = timed(step, args.steps, args.warmup, torch)
+    _, sel = _C.adaptive_attention(q, kb, kr, vb, vr, B, Hq, Hkv, S, S, d, top_k, True)
+    union = sel.view(B, Hkv, Hq // Hkv, S).amax(dim=2)        # keys whose residual is read
+    n_res = int(union.sum().item())
+    del sel, union
+    bin_bytes = 2 * B * Hkv * S * W.algorithmic_bytes_per_key(d, residual=False)
+    res_bytes = 2 * n_res * (d // 2 + 2)
+    alg = bin_bytes + res_bytes
+    wall_c = timed(lambda: _C.attention(q, kb, kr, vb, vr, B, Hq, Hkv, S, S, d),
+                   max(5, args.steps // 2), 2, torch)
+    return {
+        "metric": "adaptive top-10% decode-attn µs/step, GQA 32/8, 128K ctx, d=128, batch 16",
+        "value": round(wall * 1e6, 1), "unit": "us/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "c5: binary scores + radix top-k + attention with residual on selected keys",
+                   "batch": B, "heads": Hq, "kv_heads": Hkv, "seq_len": S, "head_dim": d,
+                   "top_k": top_k, "residual_keys_read": n_res, "bytes_per_step": alg},
+        "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "whole adaptive step (radix passes + attention), wall clock"},
+        "full_compensated_us": round(wall_c * 1e6, 1),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -130,10 +294,17 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
 
-    cfg = W.CONFIGS["c3"]
-    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.config != "c3":
+        fn = {"c2": lambda: bench_c2(args, torch, _C, W),
+              "c4": lambda: bench_c4(args, torch, _C, W, bitcache_amd),
+              "c5": lambda: bench_c5(args, torch, _C, W)}[args.config]
+        print(json.dumps(fn()), flush=True)
+        return
+
+    cfg = W.CONFIGS["c3"]
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
     q, k, v = W.make_qkv(cfg, device=dev)
     kb, kr = _C.encode_fused(k.view(-1, d), False)
     vb, vr = _C.encode_fused(v.view(-1, d), False)

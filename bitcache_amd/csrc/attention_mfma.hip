@@ -35,12 +35,14 @@ namespace {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 
 template <int D, int G>
 struct QDigits {
     uint32_t signs[G][D / 32];
     int4 digits[G][D / 8];        // .x..w = balanced int4 digits 0..3 of elements 8w..8w+7 (nibble k = element 8w+k)
+    int16_t qint[G][D];           // q_int = rint(q / dq), |q_int| <= 30583
     float scale_q[G];             // sequential mean |q| (src/compensated_attention.cu:65-67)
     float dq[G];                  // fixed-point step of q_int
 };
@@ -57,7 +59,10 @@ struct WaveLds {
     static constexpr int kSignBytes = 64 * D / 8 > 1024 ? 64 * D / 8 : 1024;
     static constexpr int kStage = kCodeBytes + kSignBytes;
     static constexpr int kWeightBytes = 2 * 2 * G * 64 * 2;
-    static constexpr int kMain = 2 * kStage + kWeightBytes;
+    // K-side residual dots of all heads, [G][64 keys] int32 (GQA groups with
+    // the residual dot on the matrix cores)
+    static constexpr int kRdBytes = G > 1 ? G * 64 * 4 : 0;
+    static constexpr int kMain = 2 * kStage + kWeightBytes + kRdBytes;
     static constexpr int kEpi = ((2 * G * D + G) * 4 + 15) / 16 * 16;
     static constexpr int kBytes = kMain > kEpi ? kMain : kEpi;
 };
@@ -109,6 +114,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         uint32_t dg[4] = {0u, 0u, 0u, 0u};
         for (int k = 0; k < 8; k++) {
             int t = (int)__builtin_rintf(qf[g * D + 8 * w + k] / qd.dq[g]);
+            qd.qint[g][8 * w + k] = (int16_t)t;
             for (int j = 0; j < 4; j++) {
                 const int d = ((t + 8) & 15) - 8;
                 dg[j] |= ((uint32_t)d & 0xFu) << (4 * k);
@@ -133,7 +139,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #endif
 template <int D, int G>
 struct Occupancy {
-    static constexpr int kWaves = (G == 1 && D <= 128) ? BC_MHA_WAVES : ((G <= 2 && D <= 128) ? 2 : 1);
+    static constexpr int kWaves = (G == 1 && D <= 128) ? BC_MHA_WAVES : (D <= 128 ? 2 : 1);
 };
 
 // Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
@@ -160,7 +166,12 @@ void attn_mfma_kernel(AttnArgs a) {
     // l%Q of key i*(64/Q) + l/Q; for K this needs a Q-lane reduction of the
     // partial dots.  The adaptive mode gathers only selected keys' codes and
     // always works per key.
-    constexpr bool LIN_K = (BC_LIN_K || G > 1) && MODE == MODE_COMP;
+    // GQA groups (d >= 128): the K residual dots of all G heads come from one
+    // set of int8 MFMAs (keys x dims times dims x (head, digit plane)); the
+    // lane holds 16-byte code pieces of 16 keys instead of one key's row
+    constexpr bool KMF = G > 1 && MODE == MODE_COMP && D >= 128;
+    constexpr int NPC = D / 128;  // 16-byte pieces per lane per 16-key block
+    constexpr bool LIN_K = (BC_LIN_K || G > 1) && MODE == MODE_COMP && !KMF;
     constexpr bool LIN_V = BC_LIN_V && MODE == MODE_COMP;
     constexpr int Q = D / 32;    // 16-byte pieces per code row
     // Vector-memory operations issued per prefetched tile, counted at their
@@ -203,6 +214,7 @@ void attn_mfma_kernel(AttnArgs a) {
 
     uint8_t* my = wave_lds[wave];
     uint16_t* wts = (uint16_t*)(my + 2 * WL::kStage);  // [2 parts][2G cols][64 slots]
+    int* rdl = (int*)(my + 2 * WL::kStage + WL::kWeightBytes);  // [G][64] residual dots
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
@@ -254,6 +266,40 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     }
 
+    // int8 MFMA B operand: column c = 2g + p is digit plane p of head g
+    // (q_int = d0 + 256 d1, d0 in [-128, 127]); slot s of lane group q for
+    // piece pc and half h is the dim that the unpacked codes put there (see
+    // the residual dot below): 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2 with
+    // r = s/4, j = s%4
+    v4i_t bq[KMF ? NPC : 1][2];
+    if constexpr (KMF) {
+        const int col = lane & 15, qg4 = lane >> 4;
+        const int gh = col >> 1, pl = col & 1;
+#pragma unroll
+        for (int pc = 0; pc < NPC; pc++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int wd[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int dim = 32 * (qg4 + 4 * pc) + 8 * (2 * h + (r >> 1)) + 2 * j + (r & 1);
+                        int v = 0;
+                        if (gh < G) {
+                            const int t = qd.qint[gh][dim];
+                            const int d0 = ((t + 128) & 255) - 128;
+                            v = pl == 0 ? d0 : (t - d0) >> 8;
+                        }
+                        word |= ((uint32_t)v & 0xFFu) << (8 * j);
+                    }
+                    wd[r] = (int)word;
+                }
+                bq[pc][h] = v4i_t{wd[0], wd[1], wd[2], wd[3]};
+            }
+    }
+
     // byte offset of the 16-byte piece `off` of a tile row plane with `rb`
     // bytes per key; pieces of keys past the range re-read key t0's row (in
     // range; their weight is 0), so every lane issues the same loads and no
@@ -275,11 +321,25 @@ void attn_mfma_kernel(AttnArgs a) {
         if constexpr (MODE == MODE_COMP) {
             r.rsk = a.kr.scales[ki];
             r.rsv = a.vr.scales[ki];
+            if constexpr (KMF) {
+                // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
 #pragma unroll
-            for (int i = 0; i < Q; i++) {
-                const uint4 c = *(const uint4*)(a.kr.codes + (LIN_K ? piece(t0, i * 1024 + 16 * lane, CB)
-                                                                    : ki * CB + 16 * i));
-                r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int pc = 0; pc < NPC; pc++) {
+                        const int sk2 = t0 + 16 * kb + (lane & 15);
+                        const int64_t kk = kv_base + (sk2 < key_end ? sk2 : t0);
+                        const uint4 c = *(const uint4*)(a.kr.codes + kk * CB + 16 * ((lane >> 4) + 4 * pc));
+                        const int i = kb * NPC + pc;
+                        r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < Q; i++) {
+                    const uint4 c = *(const uint4*)(a.kr.codes + (LIN_K ? piece(t0, i * 1024 + 16 * lane, CB)
+                                                                        : ki * CB + 16 * i));
+                    r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+                }
             }
         }
     };
@@ -390,7 +450,44 @@ void attn_mfma_kernel(AttnArgs a) {
         int racc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) racc[g] = 0;
-        if constexpr (LIN_K) {
+        if constexpr (KMF) {
+            // codes as int8 16*n (signed): low nibbles via x << 4, high nibbles in
+            // place; each half of a piece is one 16x16x64 MFMA with 16 keys x 64 dims
+            v4i_t acc[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                acc[kb] = v4i_t{0, 0, 0, 0};
+#pragma unroll
+                for (int pc = 0; pc < NPC; pc++)
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t x0 = kc[4 * (kb * NPC + pc) + 2 * h];
+                        const uint32_t x1 = kc[4 * (kb * NPC + pc) + 2 * h + 1];
+                        const v4i_t av = v4i_t{(int)((x0 << 4) & 0xF0F0F0F0u), (int)(x0 & 0xF0F0F0F0u),
+                                               (int)((x1 << 4) & 0xF0F0F0F0u), (int)(x1 & 0xF0F0F0F0u)};
+                        acc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq[pc][h], acc[kb], 0, 0, 0);
+                    }
+            }
+            // lane l holds keys 16kb + 4(l/16) + i, column l%16 = (head, plane):
+            // planes of a head are neighbouring lanes -> q_int dot * 16 on even lanes
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                int v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int hi = __builtin_amdgcn_mov_dpp(acc[kb][i], 0xB1, 0xF, 0xF, true);
+                    v[i] = acc[kb][i] + hi * 256;
+                }
+                const int col = lane & 15;
+                if ((col & 1) == 0 && col < 2 * G)
+                    *(int4*)&rdl[(col >> 1) * 64 + 16 * kb + 4 * g4] = make_int4(v[0], v[1], v[2], v[3]);
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+            for (int g = 0; g < G; g++) racc[g] = rdl[g * 64 + lane] >> 4;
+        } else if constexpr (LIN_K) {
             // round i: this lane holds 32 dims (quarter) of key i*(64/Q) + l/Q;
             // partial dots are summed over the Q lanes of the row, and the lane
             // whose own key it is keeps the total
