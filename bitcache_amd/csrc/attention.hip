@@ -83,7 +83,9 @@ __device__ void prep_queries(const uint16_t* qbase, QPrep<D>* qp, float* qf_scra
         qp[g].pairs[w][t] = lo | (hi << 16);
     }
     if (tid < G) {
+        // sequential fp32 order (element 0 first); the reads are independent
         float acc = 0.0f, sum = 0.0f;
+#pragma unroll 32
         for (int i = 0; i < D; i++) {
             acc += fabsf(qf_scratch[tid * D + i]);
             sum += qf_scratch[tid * D + i];
@@ -367,25 +369,55 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // Merge split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 // Same normalisation as the reference (acc * (l > 0 ? 1/l : 0), fp16 store,
 // src/compensated_attention.cu:104-108).
+// Merge of the split partials of one (b, query head) per block: the maximum,
+// weights f_s = 2^(m_s - M) and the total sum are reduced over the splits in
+// parallel; then P = 256 / D thread groups each sum a residue class of the
+// splits for every dimension, and the groups are added.
+constexpr int kMaxSplits = 2048;
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < nw; w++) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    return r;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* ws, uint16_t* out,
                                                            int n_splits) {
-    const int bh = blockIdx.x;
+    constexpr int P = 256 / D > 0 ? 256 / D : 1;
+    __shared__ float fsh[kMaxSplits];
+    __shared__ float red[256];
+    const int bh = blockIdx.x, tid = threadIdx.x;
     const float* p = ws + (int64_t)bh * n_splits * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; s++) M = fmaxf(M, p[s * (D + 2)]);
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float accv = 0.0f, l = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < n_splits; s++) {
-                const float ms = p[s * (D + 2)];
-                const float f = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
-                accv += f * p[s * (D + 2) + 2 + d];
-                l += f * p[s * (D + 2) + 1];
-            }
-        }
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        out[(int64_t)bh * D + d] = f2h(accv * inv);
+    float m = -INFINITY;
+    for (int s = tid; s < n_splits; s += blockDim.x) m = fmaxf(m, p[(int64_t)s * (D + 2)]);
+    const float M = block_reduce(m, true, red);
+    float l = 0.0f;
+    for (int s = tid; s < n_splits; s += blockDim.x) {
+        const float ms = p[(int64_t)s * (D + 2)];
+        const float f = (ms == -INFINITY) ? 0.0f : exp2f(ms - M);
+        fsh[s] = f;
+        l += f * p[(int64_t)s * (D + 2) + 1];
+    }
+    const float L = block_reduce(l, false, red);  // its barriers also publish fsh
+    const int part = tid / D, d = tid % D;
+    float acc = 0.0f;
+    if (part < P) {
+#pragma unroll 4
+        for (int s = part; s < n_splits; s += P) acc += fsh[s] * p[(int64_t)s * (D + 2) + 2 + d];
+    }
+    __syncthreads();
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < D) {
+        float tot = red[tid];
+        for (int q = 1; q < P; q++) tot += red[q * D + tid];
+        out[(int64_t)bh * D + tid] = f2h(L > 0.0f ? tot * (1.0f / L) : 0.0f);
     }
 }
 
@@ -663,7 +695,10 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
         return e ? atoi(e) : 0;
     }();
     if (forced > 0) want = forced;
-    int max_split = (tiles + 7) / 8;             // at least 8 tiles (2 per wave) per split
+    if (want > kMaxSplits) want = kMaxSplits;   // the combine kernel's weight table
+    // at least 16 tiles (4 per wave) per split: the per-workgroup query set-up
+    // is amortised (measured on the 16K-context GQA decode step)
+    int max_split = tiles / 16;
     if (max_split < 1) max_split = 1;
     if (want > max_split) want = max_split;
     if (want < 1) want = 1;
@@ -713,8 +748,7 @@ void launch_split_g(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t s
 
 template <int D>
 void launch_combine(const float* ws, uint16_t* out, int bh, int n_splits, hipStream_t st) {
-    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(bh), dim3(D < 256 ? D : 256), 0, st, ws, out,
-                       n_splits);
+    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(bh), dim3(256), 0, st, ws, out, n_splits);
 }
 
 #define BC_DISPATCH_D(d, FN, ...)                                           \

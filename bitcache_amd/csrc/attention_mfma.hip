@@ -43,6 +43,9 @@ struct QDigits {
     uint32_t signs[G][D / 32];
     int4 digits[G][D / 8];        // .x..w = balanced int4 digits 0..3 of elements 8w..8w+7 (nibble k = element 8w+k)
     int16_t qint[G][D];           // q_int = rint(q / dq), |q_int| <= 30583
+    // int8 MFMA B operands of the K residual dot (GQA groups, d >= 128):
+    // [piece][half][lane] (see the kernel)
+    int4 bq[(G > 1 && D >= 128) ? D / 128 : 1][2][(G > 1 && D >= 128) ? 64 : 1];
     float scale_q[G];             // sequential mean |q| (src/compensated_attention.cu:65-67)
     float dq[G];                  // fixed-point step of q_int
 };
@@ -87,16 +90,20 @@ __device__ __forceinline__ int slot_of(int k) {
     return 16 * g4 + 8 * mh + ((r & 3) << 1) + (r >> 2);
 }
 
-template <int D, int G>
+template <int D, int G, bool KMF>
 __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf) {
     const int tid = threadIdx.x;
     for (int i = tid; i < G * D; i += blockDim.x) qf[i] = h2f(qbase[i]);
     __syncthreads();
     if (tid < G) {
+        // sequential fp32 order (element 0 first); the reads are independent
         float acc = 0.0f, mx = 0.0f;
-        for (int i = 0; i < D; i++) {
-            acc += fabsf(qf[tid * D + i]);
-            mx = fmaxf(mx, fabsf(qf[tid * D + i]));
+        const float4* q4 = (const float4*)&qf[tid * D];
+#pragma unroll
+        for (int c = 0; c < D / 4; c++) {
+            const float4 v = q4[c];
+            acc += fabsf(v.x); acc += fabsf(v.y); acc += fabsf(v.z); acc += fabsf(v.w);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         qd.scale_q[tid] = acc / (float)D;
         // |q_int| <= 30583 keeps the top digit in [-8, 7]
@@ -122,6 +129,34 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
             }
         }
         qd.digits[g][w] = make_int4((int)dg[0], (int)dg[1], (int)dg[2], (int)dg[3]);
+    }
+    if constexpr (KMF) {
+        // B operand words: column c = 2g + p is digit plane p of head g
+        // (q_int = d0 + 256 d1, d0 in [-128, 127]); slot s = 4r + j of lane
+        // group q for piece pc and half h holds dim
+        // 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the unpacked codes put it
+        __syncthreads();
+        constexpr int NPC = D / 128;
+        for (int e = tid; e < NPC * 2 * 64; e += blockDim.x) {
+            const int pc = e / 128, h = (e / 64) & 1, ln = e & 63;
+            const int col = ln & 15, qg4 = ln >> 4, gh = col >> 1, pl = col & 1;
+            int wd[4];
+            for (int r = 0; r < 4; r++) {
+                uint32_t word = 0;
+                for (int j = 0; j < 4; j++) {
+                    const int dim = 32 * (qg4 + 4 * pc) + 8 * (2 * h + (r >> 1)) + 2 * j + (r & 1);
+                    int v = 0;
+                    if (gh < G) {
+                        const int t = qd.qint[gh][dim];
+                        const int d0 = ((t + 128) & 255) - 128;
+                        v = pl == 0 ? d0 : (t - d0) >> 8;
+                    }
+                    word |= ((uint32_t)v & 0xFFu) << (8 * j);
+                }
+                wd[r] = (int)word;
+            }
+            qd.bq[pc][h][ln] = make_int4(wd[0], wd[1], wd[2], wd[3]);
+        }
     }
     __syncthreads();
 }
@@ -186,7 +221,7 @@ void attn_mfma_kernel(AttnArgs a) {
     using WL = WaveLds<D, G>;
 
     __shared__ QDigits<D, G> qd;
-    __shared__ float qf[G * D];
+    __shared__ __attribute__((aligned(16))) float qf[G * D];
     __shared__ __attribute__((aligned(16))) uint8_t wave_lds[4][WL::kBytes];
     __shared__ float wm[4][G], wlsum[4][G], wsc[4];
 
@@ -198,7 +233,7 @@ void attn_mfma_kernel(AttnArgs a) {
     const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
     const int bhq0 = b * a.Hq + hq0;
 
-    prep_digits<D, G>(a.q + (int64_t)bhq0 * D, qd, qf);
+    prep_digits<D, G, KMF>(a.q + (int64_t)bhq0 * D, qd, qf);
 
     // the wave index is uniform: readfirstlane lets the compiler keep the tile
     // loop in scalar registers (a uniform loop, not an exec-masked one)
@@ -266,37 +301,15 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     }
 
-    // int8 MFMA B operand: column c = 2g + p is digit plane p of head g
-    // (q_int = d0 + 256 d1, d0 in [-128, 127]); slot s of lane group q for
-    // piece pc and half h is the dim that the unpacked codes put there (see
-    // the residual dot below): 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2 with
-    // r = s/4, j = s%4
+    // int8 MFMA B operands of the K residual dot (loop invariant)
     v4i_t bq[KMF ? NPC : 1][2];
     if constexpr (KMF) {
-        const int col = lane & 15, qg4 = lane >> 4;
-        const int gh = col >> 1, pl = col & 1;
 #pragma unroll
         for (int pc = 0; pc < NPC; pc++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                int wd[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    uint32_t word = 0;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int dim = 32 * (qg4 + 4 * pc) + 8 * (2 * h + (r >> 1)) + 2 * j + (r & 1);
-                        int v = 0;
-                        if (gh < G) {
-                            const int t = qd.qint[gh][dim];
-                            const int d0 = ((t + 128) & 255) - 128;
-                            v = pl == 0 ? d0 : (t - d0) >> 8;
-                        }
-                        word |= ((uint32_t)v & 0xFFu) << (8 * j);
-                    }
-                    wd[r] = (int)word;
-                }
-                bq[pc][h] = v4i_t{wd[0], wd[1], wd[2], wd[3]};
+                const int4 w = qd.bq[pc][h][lane];
+                bq[pc][h] = v4i_t{w.x, w.y, w.z, w.w};
             }
     }
 
