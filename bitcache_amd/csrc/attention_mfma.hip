@@ -204,7 +204,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // GQA groups (d >= 128): the K residual dots of all G heads come from one
     // set of int8 MFMAs (keys x dims times dims x (head, digit plane)); the
     // lane holds 16-byte code pieces of 16 keys instead of one key's row
-    constexpr bool KMF = G > 1 && MODE == MODE_COMP && D >= 128;
+    constexpr bool KMF = G > 1 && RES && D >= 128;
     constexpr int NPC = D / 128;  // 16-byte pieces per lane per 16-key block
     constexpr bool LIN_K = (BC_LIN_K || G > 1) && MODE == MODE_COMP && !KMF;
     constexpr bool LIN_V = BC_LIN_V && MODE == MODE_COMP;
@@ -439,11 +439,13 @@ void attn_mfma_kernel(AttnArgs a) {
             if (selmask) {
                 rsk = h2f(a.kr.scales[ki]);
                 rsv = h2f(a.vr.scales[ki]);
-                const uint4* cp = (const uint4*)(a.kr.codes + ki * CB);
+                if constexpr (!KMF) {
+                    const uint4* cp = (const uint4*)(a.kr.codes + ki * CB);
 #pragma unroll
-                for (int i = 0; i < CW / 4; i++) {
-                    const uint4 c = cp[i];
-                    kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
+                    for (int i = 0; i < CW / 4; i++) {
+                        const uint4 c = cp[i];
+                        kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
+                    }
                 }
                 const uint8_t* vc = a.vr.codes + ki * CB;
 #pragma unroll
@@ -457,6 +459,25 @@ void attn_mfma_kernel(AttnArgs a) {
                 for (int g = 0; g < G; g++)
                     a.selected[(int64_t)(bhq0 + g) * a.S + s] = (selmask >> g) & 1u;
             }
+            if constexpr (KMF) {
+                // code pieces (matrix-core layout) of the keys any head selected
+                const uint64_t anysel = __ballot(selmask != 0u);
+                if (anysel != 0ull) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; kb++) {
+                        const int key = 16 * kb + (lane & 15);
+                        if ((anysel >> key) & 1ull) {
+                            const int64_t kk = kv_base + t0 + key;
+#pragma unroll
+                            for (int pc = 0; pc < NPC; pc++) {
+                                const uint4 c = *(const uint4*)(a.kr.codes + kk * CB + 16 * ((lane >> 4) + 4 * pc));
+                                const int i = kb * NPC + pc;
+                                kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
+                            }
+                        }
+                    }
+                }
+            }
         }
 
         // residual dot on the raw int4 codes: sum_i q_int_i * n_i per head
@@ -464,8 +485,12 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) racc[g] = 0;
         if constexpr (KMF) {
+          bool kmf_run = true;
+          if constexpr (MODE == MODE_ADAPTIVE) kmf_run = __ballot(selmask != 0u) != 0ull;
+          if (kmf_run) {
             // codes as int8 16*n (signed): low nibbles via x << 4, high nibbles in
             // place; each half of a piece is one 16x16x64 MFMA with 16 keys x 64 dims
+            // (rows of keys whose codes were not loaded are never used)
             v4i_t acc[4];
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
@@ -500,6 +525,7 @@ void attn_mfma_kernel(AttnArgs a) {
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
             for (int g = 0; g < G; g++) racc[g] = rdl[g * 64 + lane] >> 4;
+          }
         } else if constexpr (LIN_K) {
             // round i: this lane holds 32 dims (quarter) of key i*(64/Q) + l/Q;
             // partial dots are summed over the Q lanes of the row, and the lane
