@@ -138,6 +138,135 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-parallel encoder for d in {64, 128, 256}: L = d/8 lanes per vector, each
+// lane holding 8 consecutive elements (one 16-byte load), so a wave encodes
+// 64/L vectors at once with coalesced loads and stores and all reductions on
+// DPP / swizzle lane moves.  Same arithmetic as encode_kernel: the scale sum
+// follows the reference tree exactly -- element t = 8j + k sits in lane j, so
+// the tree levels s = 64..8 pair lane j with lane j + s/8 (row_shl) and the
+// levels s = 4, 2, 1 are in-lane; d = 256 first adds |x_{t+128}| from the
+// lane 16 above (the reference's per-thread loop), d = 64 skips the s = 64
+// level (it adds +0.0).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                  0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+template <int PAT>
+__device__ __forceinline__ float swz_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), PAT));
+}
+
+template <int D, int MODE>
+__global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1) {
+    static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
+    constexpr int L = D / 8;        // lanes per vector
+    constexpr int VPW = 64 / L;     // vectors per wave
+    // swizzle pattern that broadcasts lane 0 of each L-lane group (and-mask mode)
+    constexpr int BCAST = L == 8 ? 0x18 : (L == 16 ? 0x10 : 0x00);
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / L, j = lane % L;
+    const int64_t wave_id = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+#pragma unroll 1
+    for (int jb = 0; jb < 2; jb++) {
+        const EncodeJob& J = jb ? j1 : j0;
+        for (int64_t base = wave_id * VPW; base < J.n; base += nwaves * VPW) {
+            const int64_t v0 = base + sub;
+            const bool live = v0 < J.n;
+            const int64_t v = live ? v0 : J.n - 1;
+            const int64_t dv = J.row_len == 1 ? v * J.row_stride + J.row_offset
+                                              : (v / J.row_len) * J.row_stride + J.row_offset + v % J.row_len;
+            const uint4 raw = ((const uint4*)(J.src + v * D))[j];
+            const uint32_t hw[4] = {raw.x, raw.y, raw.z, raw.w};
+            float x[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) x[k] = h2f((uint16_t)(hw[k >> 1] >> (16 * (k & 1))));
+
+            uint32_t byte = 0;
+            float s;
+            float mean = 0.0f;
+            if constexpr (MODE == ENC_RESIDUAL_ONLY) {
+                byte = J.sign_plane[dv * (D / 8) + j];
+                s = h2f(J.scale_plane[dv]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; k++) byte |= (x[k] >= 0.0f ? 1u : 0u) << k;  // +-0 -> 1, NaN -> 0
+                float p[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]);
+                if constexpr (D == 256) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) p[k] = p[k] + swz_f<0x401F>(p[k]);  // + |x_{t+128}|
+                }
+                if constexpr (D >= 128) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x108>(p[k]);   // s = 64
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);       // s = 32
+#pragma unroll
+                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x102>(p[k]);       // s = 16
+#pragma unroll
+                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x101>(p[k]);       // s = 8
+#pragma unroll
+                for (int k = 0; k < 4; k++) p[k] = p[k] + p[k + 4];                  // s = 4
+                p[0] = p[0] + p[2];
+                p[1] = p[1] + p[3];                                                   // s = 2
+                p[0] = p[0] + p[1];                                                   // s = 1
+                const float total_abs = swz_f<BCAST>(p[0]);
+                mean = total_abs / (float)D;
+                if constexpr (MODE == ENC_FUSED_FP16) s = h2f(f2h(mean));
+                else s = mean;
+                // sign bytes of 4 lanes -> one little-endian word
+                const uint32_t w = byte | (dpp_u<0x101>(byte) << 8) | (dpp_u<0x102>(byte) << 16) |
+                                   (dpp_u<0x103>(byte) << 24);
+                if (live) {
+                    if ((j & 3) == 0) ((uint32_t*)(J.sign_plane + dv * (D / 8)))[j >> 2] = w;
+                    if (j == 0) J.scale_plane[dv] = f2h(mean);
+                }
+            }
+
+            if constexpr (MODE != ENC_BINARY) {
+                if (J.code_plane == nullptr) continue;
+                float r[8];
+                float m = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    r[k] = x[k] - (((byte >> k) & 1u) ? s : -s);
+                    m = fmaxf(m, fabsf(r[k]));
+                }
+                // fmaxf ignores NaN and is order independent (src/residual.cu:201-223)
+                if constexpr (L == 8) {
+                    m = fmaxf(m, dpp_f<0x141>(m));   // half mirror
+                    m = fmaxf(m, dpp_f<0x4E>(m));    // quad 2,3,0,1
+                    m = fmaxf(m, dpp_f<0xB1>(m));    // quad 1,0,3,2
+                } else {
+                    m = fmaxf(m, dpp_f<0x128>(m));   // row rotations
+                    m = fmaxf(m, dpp_f<0x124>(m));
+                    m = fmaxf(m, dpp_f<0x122>(m));
+                    m = fmaxf(m, dpp_f<0x121>(m));
+                    if constexpr (L == 32) m = fmaxf(m, swz_f<0x401F>(m));
+                }
+                const float absmax = m;
+                const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
+                uint32_t word = 0;
+#pragma unroll
+                for (int k = 0; k < 8; k++) word |= ((uint32_t)quant7(r[k] * inv) & 0xFu) << (4 * k);
+                if (live) {
+                    ((uint32_t*)(J.code_plane + dv * (D / 2)))[j] = word;
+                    if (j == 0) J.rscale_plane[dv] = f2h(absmax);
+                }
+            }
+        }
+    }
+}
+
 int grid_for(int64_t nvec) {
     const int64_t want = (nvec + 3) / 4;
     const int64_t cap = (int64_t)bc::device_cu_count() * 32;
@@ -146,6 +275,20 @@ int grid_for(int64_t nvec) {
 
 template <int MODE>
 int launch_encode(int d, const EncodeJob& a, const EncodeJob& b, hipStream_t st) {
+    if (d == 64 || d == 128 || d == 256) {
+        // row encoder: 64/L vectors per wave, 4 waves per block, grid-stride
+        const int64_t vpb = 4 * (64 / (d / 8));
+        const int64_t want = (a.n + b.n + vpb - 1) / vpb;
+        const int64_t cap = (int64_t)bc::device_cu_count() * 16;
+        const int grid = (int)(want < cap ? (want < 1 ? 1 : want) : cap);
+        if (d == 64)
+            hipLaunchKernelGGL((encode_rows_kernel<64, MODE>), dim3(grid), dim3(256), 0, st, a, b);
+        else if (d == 128)
+            hipLaunchKernelGGL((encode_rows_kernel<128, MODE>), dim3(grid), dim3(256), 0, st, a, b);
+        else
+            hipLaunchKernelGGL((encode_rows_kernel<256, MODE>), dim3(grid), dim3(256), 0, st, a, b);
+        return bc::check_launch("encode");
+    }
     const int grid = grid_for(a.n + b.n);
     switch (d) {
 #define BC_CASE(DD)                                                                       \
