@@ -701,18 +701,36 @@ void attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        // sign part: rows = dims 64h + 4*lj + p
+        // all transposed reads of the tile first (they retire in order while
+        // the MFMAs of earlier blocks run)
         const int row_key = 16 * g4 + lj;  // this lane addresses row (key) lj of its group
+        bool any_sel = true;
+        if constexpr (MODE == MODE_ADAPTIVE) any_sel = __ballot(selmask != 0u) != 0ull;
+        v2i_t wsg[NH];
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+            wsg[h] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, st_signs + SB * row_key + 8 * h));
+        v2i_t wrs[RES ? NB : 1];
+        if constexpr (RES) {
+            if (any_sel) {
+#pragma unroll
+                for (int db = 0; db < NB; db++) {
+                    const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 8 * db
+                                              : st_codes + (db >> 1) * 1024 + 16 * row_key + 8 * (db & 1);
+                    wrs[db] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
+                }
+            }
+        }
+
+        // sign part: rows = dims 64h + 4*lj + p
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            const uint8_t* rp = st_signs + SB * row_key + 8 * h;
-            const v2i_t w = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
 #pragma unroll
             for (int mh = 0; mh < 2; mh++) {
                 // x holds nibble r of key r (r = 0..3) and of key r + 4 (bits
                 // 16 + 4r): pair word k keeps bit p of keys k and k + 4 in place,
                 // an fp16 subnormal 2^(4(k&1) + p - 24); keys 2, 3 via x >> 8
-                const uint32_t x = (uint32_t)(mh ? w.y : w.x);
+                const uint32_t x = (uint32_t)(mh ? wsg[h].y : wsg[h].x);
                 const uint32_t y = x >> 8;
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
@@ -724,24 +742,18 @@ void attn_mfma_kernel(AttnArgs a) {
                     const h8_t av = __builtin_bit_cast(h8_t, pw);
                     cs[h][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bsig[mh], cs[h][p], 0, 0, 0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
         }
 
         // residual part: rows = dims 16db + lj
         if constexpr (RES) {
-            bool any_sel = true;
-            if constexpr (MODE == MODE_ADAPTIVE) any_sel = __ballot(selmask != 0u) != 0ull;
             if (any_sel) {
 #pragma unroll
                 for (int db = 0; db < NB; db++) {
-                    const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 8 * db
-                                            : st_codes + (db >> 1) * 1024 + 16 * row_key + 8 * (db & 1);
-                    const v2i_t w = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
 #pragma unroll
                     for (int mh = 0; mh < 2; mh++) {
                         // u = n + 8 in place: keys k, k + 4 at 4(k&1) (odd keys 16x)
-                        const uint32_t x = (uint32_t)(mh ? w.y : w.x) ^ 0x88888888u;
+                        const uint32_t x = (uint32_t)(mh ? wrs[db].y : wrs[db].x) ^ 0x88888888u;
                         const uint32_t y = x >> 8;
                         uint32_t pw[4];
                         pw[0] = x & 0x000F000Fu;
@@ -751,7 +763,6 @@ void attn_mfma_kernel(AttnArgs a) {
                         const h8_t av = __builtin_bit_cast(h8_t, pw);
                         cn[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bres[mh], cn[db], 0, 0, 0);
                     }
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }

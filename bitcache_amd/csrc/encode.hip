@@ -148,20 +148,6 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
 // levels s = 4, 2, 1 are in-lane; d = 256 first adds |x_{t+128}| from the
 // lane 16 above (the reference's per-thread loop), d = 64 skips the s = 64
 // level (it adds +0.0).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
-                                                                  0xF, 0xF, true));
-}
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
-}
-template <int PAT>
-__device__ __forceinline__ float swz_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), PAT));
-}
-
 template <int D, int MODE>
 __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
