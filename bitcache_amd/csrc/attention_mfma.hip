@@ -53,10 +53,11 @@ struct QDigits {
 // Per-wave LDS: two V staging buffers (tile i is consumed while tile i+1
 // lands), each the tile's code bytes then its sign bytes, then the (hi, lo)
 // fp16 weight columns [part][2G][64 slots].  The epilogue
-// reuses the region for [2 parts][G][D] partial sums + G offsets.
-template <int D, int G>
+// reuses the region for [parts][G][D] partial sums (sign part, plus the
+// residual part when present) + G offsets.  Binary attention stages no codes.
+template <int D, int G, bool RES>
 struct WaveLds {
-    static constexpr int kCodeBytes = 64 * D / 2;
+    static constexpr int kCodeBytes = RES ? 64 * D / 2 : 0;
     // D = 64: 8-byte sign rows are copied two keys per lane by all 64 lanes
     // (lanes 32..63 repeat lanes 0..31 into the second half), hence 1 KB
     static constexpr int kSignBytes = 64 * D / 8 > 1024 ? 64 * D / 8 : 1024;
@@ -64,9 +65,9 @@ struct WaveLds {
     static constexpr int kWeightBytes = 2 * 2 * G * 64 * 2;
     // K-side residual dots of all heads, [G][64 keys] int32 (GQA groups with
     // the residual dot on the matrix cores)
-    static constexpr int kRdBytes = G > 1 ? G * 64 * 4 : 0;
+    static constexpr int kRdBytes = (G > 1 && RES) ? G * 64 * 4 : 0;
     static constexpr int kMain = 2 * kStage + kWeightBytes + kRdBytes;
-    static constexpr int kEpi = ((2 * G * D + G) * 4 + 15) / 16 * 16;
+    static constexpr int kEpi = (((RES ? 2 : 1) * G * D + G) * 4 + 15) / 16 * 16;
     static constexpr int kBytes = kMain > kEpi ? kMain : kEpi;
 };
 
@@ -172,9 +173,14 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_LIN_V
 #define BC_LIN_V 1
 #endif
-template <int D, int G>
+#ifndef BC_BIN_WAVES
+#define BC_BIN_WAVES 5
+#endif
+template <int D, int G, int MODE>
 struct Occupancy {
-    static constexpr int kWaves = (G == 1 && D <= 128) ? BC_MHA_WAVES : (D <= 128 ? 2 : 1);
+    static constexpr int kWaves =
+        MODE == MODE_BINARY ? (D <= 128 ? (G <= 2 ? BC_BIN_WAVES : 3) : 2)
+                            : ((G == 1 && D <= 128) ? BC_MHA_WAVES : (D <= 128 ? 2 : 1));
 };
 
 // Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
@@ -187,7 +193,7 @@ __device__ __forceinline__ int row_group_sum(int v) {
 }
 
 template <int D, int G, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<D, G>::kWaves)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<D, G, MODE>::kWaves)))
 void attn_mfma_kernel(AttnArgs a) {
     constexpr int NB = D / 16;   // nibble dim-blocks (16 dims each)
     constexpr int NH = D / 64;   // sign blocks (64 dims each)
@@ -218,7 +224,7 @@ void attn_mfma_kernel(AttnArgs a) {
     constexpr int kKLoads = (SB + 15) / 16 + (MODE == MODE_COMP ? 4 + Q : 2);
     constexpr int kPrefetchOps = kVDma + kKLoads;
     static_assert(kPrefetchOps + kVDma < 64, "vmcnt holds 6 bits");
-    using WL = WaveLds<D, G>;
+    using WL = WaveLds<D, G, RES>;
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
@@ -813,7 +819,7 @@ void attn_mfma_kernel(AttnArgs a) {
             wm[wave][g] = m[g];
             wlsum[wave][g] = l_w;
             wsc[wave] = ldexpf(1.0f, -wexp);
-            accw[2 * G * D + g] = o_w;  // stash after the arrays
+            accw[(RES ? 2 : 1) * G * D + g] = o_w;  // stash after the arrays
         }
     }
     // hi + lo columns are adjacent lanes (col 2g, 2g+1)
@@ -855,7 +861,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 const float* aw = (const float*)wave_lds[w];
                 float v = aw[(0 * G + g) * D + e];
                 if (RES) v += aw[(1 * G + g) * D + e];
-                v = (v * two24 - aw[2 * G * D + g]) * wsc[w];
+                v = (v * two24 - aw[(RES ? 2 : 1) * G * D + g]) * wsc[w];
                 accv += f * v;
                 lv += f * wlsum[w][g];
             }
