@@ -55,7 +55,7 @@ struct QDigits {
 // fp16 weight columns [part][2G][64 slots].  The epilogue
 // reuses the region for [parts][G][D] partial sums (sign part, plus the
 // residual part when present) + G offsets.  Binary attention stages no codes.
-template <int D, int G, bool RES>
+template <int D, int G, bool RES, int NSTAGE>
 struct WaveLds {
     static constexpr int kCodeBytes = RES ? 64 * D / 2 : 0;
     // D = 64: 8-byte sign rows are copied two keys per lane by all 64 lanes
@@ -66,7 +66,7 @@ struct WaveLds {
     // K-side residual dots of all heads, [G][64 keys] int32 (GQA groups with
     // the residual dot on the matrix cores)
     static constexpr int kRdBytes = (G > 1 && RES) ? G * 64 * 4 : 0;
-    static constexpr int kMain = 2 * kStage + kWeightBytes + kRdBytes;
+    static constexpr int kMain = NSTAGE * kStage + kWeightBytes + kRdBytes;
     static constexpr int kEpi = (((RES ? 2 : 1) * G * D + G) * 4 + 15) / 16 * 16;
     static constexpr int kBytes = kMain > kEpi ? kMain : kEpi;
 };
@@ -173,6 +173,9 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_LIN_V
 #define BC_LIN_V 1
 #endif
+#ifndef BC_GQA_PIPE
+#define BC_GQA_PIPE 0
+#endif
 #ifndef BC_BIN_WAVES
 #define BC_BIN_WAVES 5
 #endif
@@ -180,7 +183,8 @@ template <int D, int G, int MODE>
 struct Occupancy {
     static constexpr int kWaves =
         MODE == MODE_BINARY ? (D <= 128 ? (G <= 2 ? BC_BIN_WAVES : 3) : 2)
-                            : ((G == 1 && D <= 128) ? BC_MHA_WAVES : (D <= 128 ? 2 : 1));
+                            : ((G == 1 && D <= 128) ? BC_MHA_WAVES
+                                                    : (D <= 128 ? (G <= 4 && MODE == MODE_COMP && !BC_GQA_PIPE ? 3 : 2) : 1));
 };
 
 // Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
@@ -224,7 +228,11 @@ void attn_mfma_kernel(AttnArgs a) {
     constexpr int kKLoads = (SB + 15) / 16 + (MODE == MODE_COMP ? 4 + Q : 2);
     constexpr int kPrefetchOps = kVDma + kKLoads;
     static_assert(kPrefetchOps + kVDma < 64, "vmcnt holds 6 bits");
-    using WL = WaveLds<D, G, RES>;
+    // GQA groups in compensated mode run without the one-tile prefetch: one
+    // staging buffer and one K register set leave room for a third workgroup
+    // per CU (measured faster); adaptive mode keeps it
+    constexpr bool PIPE = G == 1 || MODE == MODE_ADAPTIVE || BC_GQA_PIPE;
+    using WL = WaveLds<D, G, RES, PIPE ? 2 : 1>;
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
@@ -254,8 +262,8 @@ void attn_mfma_kernel(AttnArgs a) {
     const int quarter = lane % Q;
 
     uint8_t* my = wave_lds[wave];
-    uint16_t* wts = (uint16_t*)(my + 2 * WL::kStage);  // [2 parts][2G cols][64 slots]
-    int* rdl = (int*)(my + 2 * WL::kStage + WL::kWeightBytes);  // [G][64] residual dots
+    uint16_t* wts = (uint16_t*)(my + (PIPE ? 2 : 1) * WL::kStage);  // [2 parts][2G cols][64 slots]
+    int* rdl = (int*)((uint8_t*)wts + WL::kWeightBytes);  // [G][64] residual dots
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
@@ -407,7 +415,7 @@ void attn_mfma_kernel(AttnArgs a) {
         // loads and the whole next-tile prefetch.  An explicit count keeps the
         // compiler from draining the queue (with direct-to-LDS loads pending it
         // would wait for zero).
-        if constexpr (MODE != MODE_ADAPTIVE) {
+        if constexpr (MODE != MODE_ADAPTIVE && PIPE) {
             constexpr int n = kVDma + kPrefetchOps;
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
@@ -683,7 +691,7 @@ void attn_mfma_kernel(AttnArgs a) {
         // this tile's V data must be in LDS: everything but the next tile's
         // loads (the youngest kPrefetchOps vector-memory operations) completes
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (MODE != MODE_ADAPTIVE) {
+        if constexpr (MODE != MODE_ADAPTIVE && PIPE) {
             constexpr int n = kPrefetchOps;
             __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
         } else {
@@ -782,7 +790,16 @@ void attn_mfma_kernel(AttnArgs a) {
     // prefetch after a wave's last tile re-reads that tile (harmless, cached)
     // so that no load sits behind a branch.
     int t = key_begin + wave * 64;
-    if (t < key_end) {
+    if (!PIPE) {
+        for (; t < key_end; t += 4 * 64) {
+            KRegs<D> ka;
+            load_k(ka, t);
+            issue_v(0, t);
+            process(ka, t, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+    } else if (t < key_end) {
         KRegs<D> ka, kb;
         load_k(ka, t);
         issue_v(0, t);
