@@ -422,20 +422,41 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* ws, uint
 }
 
 // ---------------------------------------------------------------- fp16 reference
-// Exact attention over dense fp16 K/V [B, Hkv, S, D] with fp32 accumulation.
-// Same split/online-softmax structure; q.k via v_dot2_f32_f16 on fp16 pairs,
-// p*v via mixed-precision FMA.
+// Exact attention over dense fp16 K/V [B, Hkv, S, D] with fp32 accumulation,
+// the same split / online-softmax structure and partial format as the
+// compressed kernels.  A key row (2D bytes) is read by LPR = D/8 lanes, 16
+// bytes each, so every load instruction covers whole rows (64 lanes = 1 KiB);
+// a wave takes NR such loads of K and of V per tile (TK = NR * 64/LPR keys).
+// q.k: 4 v_dot2_f32_f16 per lane and a sum over the row's lanes (DPP);
+// softmax with lane = key; p*v: 8 mixed-precision FMAs per lane, reduced over
+// the rows of the tile once at the end.
+template <int LPR>
+__device__ __forceinline__ float row_sum_f(float v) {
+    if constexpr (LPR == 8) {
+        v += dpp_f<0x141>(v);   // half mirror
+        v += dpp_f<0x4E>(v);
+        v += dpp_f<0xB1>(v);
+    } else {
+        v += dpp_f<0x128>(v);
+        v += dpp_f<0x124>(v);
+        v += dpp_f<0x122>(v);
+        v += dpp_f<0x121>(v);
+        if constexpr (LPR == 32) v += swz_f<0x401F>(v);
+    }
+    return v;
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const uint16_t* K,
                                                        const uint16_t* V, int Hq, int Hkv, int S,
                                                        int n_splits, int chunk, float* ws) {
-    constexpr int LPK = D / 8;   // value lanes per key: 8 dims (one uint4) each
-    constexpr int R = 64 / LPK;
-    constexpr int KPL = (64 + R - 1) / R;
+    constexpr int LPR = D / 8;           // lanes per key row
+    constexpr int RPI = 64 / LPR;        // rows per load instruction
+    constexpr int NR = 8;                // loads of K (and of V) per tile
+    constexpr int TK = NR * RPI;         // keys per tile
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    __shared__ uint32_t qpair[G][D / 2];
-    __shared__ float wl[4][G][64];
-    __shared__ float red[4][64][9];
+    __shared__ float sc[4][G][64];
+    __shared__ float red[4][RPI][D];
     __shared__ float wsum[4][G][D];
     __shared__ float wm[4][G], wlsum[4][G];
 
@@ -446,73 +467,82 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
     const int b = bkv / Hkv, kvh = bkv % Hkv;
     const int hq0 = kvh * (Hq / Hkv) + qg * G;
     const int bhq0 = b * Hq + hq0;
-    for (int i = threadIdx.x; i < G * D / 2; i += blockDim.x)
-        qpair[i / (D / 2)][i % (D / 2)] = ((const uint32_t*)(q + (int64_t)bhq0 * D))[i];
-    __syncthreads();
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int row = lane / LPR, part = lane % LPR;
     const int key_begin = split * chunk, key_end = min(S, key_begin + chunk);
     const int64_t base = (int64_t)bkv * S;
     const float isd2 = (1.0f / sqrtf((float)D)) * kLog2e;
-    const int vc = lane % LPK, vr = lane / LPK;
-    float m[G], lsum[G], acc[G][8];
+
+    h2 qp[G][4];   // this lane's 8 query dims (part*8 ..) per head
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const uint4 w = ((const uint4*)(q + (int64_t)(bhq0 + g) * D))[part];
+        qp[g][0] = __builtin_bit_cast(h2, w.x);
+        qp[g][1] = __builtin_bit_cast(h2, w.y);
+        qp[g][2] = __builtin_bit_cast(h2, w.z);
+        qp[g][3] = __builtin_bit_cast(h2, w.w);
+    }
+    float m[G], lp[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         m[g] = -INFINITY;
-        lsum[g] = 0.0f;
+        lp[g] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
     }
-    for (int t0 = key_begin + wave * 64; t0 < key_end; t0 += 256) {
-        uint4 vv[KPL];
+    for (int t0 = key_begin + wave * TK; t0 < key_end; t0 += 4 * TK) {
+        uint4 kr[NR], vr[NR];
 #pragma unroll
-        for (int k = 0; k < KPL; k++) {
-            const int sl = vr + R * k, s = t0 + sl;
-            vv[k] = make_uint4(0, 0, 0, 0);
-            if (vr < R && sl < 64 && s < key_end) vv[k] = ((const uint4*)(V + (base + s) * D))[vc];
+        for (int i = 0; i < NR; i++) {
+            const int key = t0 + i * RPI + row;
+            const int64_t ki = base + (key < key_end ? key : t0);
+            kr[i] = ((const uint4*)(K + ki * D))[part];
+            vr[i] = ((const uint4*)(V + ki * D))[part];
         }
-        const int s = t0 + lane;
-        const bool valid = s < key_end;
-        const uint4* kp = (const uint4*)(K + (base + (valid ? s : t0)) * D);
-        float dots[G];
+        // scores -> LDS (lane = key)
 #pragma unroll
-        for (int g = 0; g < G; g++) dots[g] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < D / 8; i++) {
-            const uint4 kk = kp[i];
+        for (int i = 0; i < NR; i++) {
+            const bool valid = t0 + i * RPI + row < key_end;
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 0]), __builtin_bit_cast(h2, kk.x), dots[g], false);
-                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 1]), __builtin_bit_cast(h2, kk.y), dots[g], false);
-                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 2]), __builtin_bit_cast(h2, kk.z), dots[g], false);
-                dots[g] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, qpair[g][4 * i + 3]), __builtin_bit_cast(h2, kk.w), dots[g], false);
+                float d = 0.0f;
+                d = __builtin_amdgcn_fdot2(qp[g][0], __builtin_bit_cast(h2, kr[i].x), d, false);
+                d = __builtin_amdgcn_fdot2(qp[g][1], __builtin_bit_cast(h2, kr[i].y), d, false);
+                d = __builtin_amdgcn_fdot2(qp[g][2], __builtin_bit_cast(h2, kr[i].z), d, false);
+                d = __builtin_amdgcn_fdot2(qp[g][3], __builtin_bit_cast(h2, kr[i].w), d, false);
+                d = row_sum_f<LPR>(d);
+                if (part == 0) sc[wave][g][i * RPI + row] = valid ? d * isd2 : -INFINITY;
             }
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // online softmax over the tile (lane = key; lanes >= TK hold no key)
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float s2 = valid ? dots[g] * isd2 : -INFINITY;
+            const float s2 = lane < TK ? sc[wave][g][lane] : -INFINITY;
             const float mn = fmaxf(m[g], wave_max(s2));
             if (mn > m[g]) {
                 const float alpha = exp2f(m[g] - mn);
-                lsum[g] *= alpha;
+                lp[g] *= alpha;
 #pragma unroll
                 for (int e = 0; e < 8; e++) acc[g][e] *= alpha;
                 m[g] = mn;
             }
-            const float p = valid ? exp2f(s2 - mn) : 0.0f;
-            lsum[g] += p;
-            wl[wave][g][lane] = p;
+            const float p = s2 == -INFINITY ? 0.0f : exp2f(s2 - mn);
+            lp[g] += p;
+            if (lane < TK) sc[wave][g][lane] = p;
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // p * v: this lane's 8 dims of the keys of its row
 #pragma unroll
-        for (int k = 0; k < KPL; k++) {
-            const int sl = vr + R * k;
-            if (!(vr < R && sl < 64 && t0 + sl < key_end)) continue;
-            const uint32_t vw[4] = {vv[k].x, vv[k].y, vv[k].z, vv[k].w};
+        for (int i = 0; i < NR; i++) {
+            const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float p = wl[wave][g][sl];
+                const float p = sc[wave][g][i * RPI + row];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const h2 hv = __builtin_bit_cast(h2, vw[e]);
@@ -521,25 +551,28 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
                 }
             }
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     }
+    // per wave: sum the rows, then combine the 4 waves
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        const float l_w = wave_sum(lsum[g]);
+        const float l_w = wave_sum(lp[g]);
         if (lane == 0) {
             wm[wave][g] = m[g];
             wlsum[wave][g] = l_w;
         }
 #pragma unroll
-        for (int e = 0; e < 8; e++) red[wave][lane][e] = acc[g][e];
+        for (int e = 0; e < 8; e++) red[wave][row][part * 8 + e] = acc[g][e];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         for (int i = lane; i < D; i += 64) {
-            const int c = i / 8, e = i % 8;
             float sum = 0.0f;
-            for (int r = 0; r < R; r++) sum += red[wave][r * LPK + c][e];
+            for (int r = 0; r < RPI; r++) sum += red[wave][r][i];
             wsum[wave][g][i] = sum;
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();

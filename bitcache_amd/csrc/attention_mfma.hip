@@ -173,6 +173,9 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_LIN_V
 #define BC_LIN_V 1
 #endif
+#ifndef BC_MHA_PIPE
+#define BC_MHA_PIPE 1
+#endif
 #ifndef BC_GQA_PIPE
 #define BC_GQA_PIPE 0
 #endif
@@ -231,7 +234,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // GQA groups in compensated mode run without the one-tile prefetch: one
     // staging buffer and one K register set leave room for a third workgroup
     // per CU (measured faster); adaptive mode keeps it
-    constexpr bool PIPE = G == 1 || MODE == MODE_ADAPTIVE || BC_GQA_PIPE;
+    constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || MODE == MODE_ADAPTIVE || BC_GQA_PIPE;
     using WL = WaveLds<D, G, RES, PIPE ? 2 : 1>;
 
     __shared__ QDigits<D, G> qd;
