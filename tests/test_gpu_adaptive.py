@@ -38,6 +38,9 @@ CASES = [
     (1, 2, 2, 2000, 128, 200, True),
     (1, 2, 2, 2000, 128, 1, True),
     (1, 2, 2, 130, 256, 13, False),
+    (1, 8, 2, 900, 256, 90, False),     # GQA 4 at d = 256
+    (1, 4, 2, 1500, 128, 150, True),    # GQA 2 with ties
+    (1, 16, 2, 640, 128, 64, False),    # GQA 8
 ]
 
 

@@ -45,6 +45,10 @@ SHAPES = [
     (2, 8, 2, 1000, 128),     # GQA 4
     (1, 8, 1, 513, 128),      # GQA 8
     (1, 6, 2, 300, 128),      # GQA 3 (query heads processed one by one)
+    (1, 4, 2, 700, 128),      # GQA 2 (int8-MFMA residual dots)
+    (2, 8, 2, 333, 64),       # GQA 4 at d = 64 (lane-piece residual dots)
+    (1, 8, 2, 500, 256),      # GQA 4 at d = 256 (two code pieces per lane)
+    (1, 16, 2, 300, 256),     # GQA 8 at d = 256
     (1, 4, 4, 777, 256),
     (1, 2, 2, 300, 96),
     (1, 3, 3, 2000, 160),
@@ -73,21 +77,22 @@ def test_compensated_and_binary_vs_oracle(F, shape):
     close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
 
 
-def test_kv_stride_and_zero_length(F):
-    say("case kv_stride")
-    B, H, S, stride, d = 2, 4, 100, 160, 128
-    q, k, v = make(B, H, H, stride, d, seed=3)
+@pytest.mark.parametrize("H,Hkv,d", [(4, 4, 128), (8, 2, 128), (8, 2, 256)])
+def test_kv_stride_and_zero_length(F, H, Hkv, d):
+    say(f"case kv_stride H={H} Hkv={Hkv} d={d}")
+    B, S, stride = 2, 100, 160
+    q, k, v = make(B, H, Hkv, stride, d, seed=3)
     kb, kr = encode_gpu(F, k)
     vb, vr = encode_gpu(F, v)
     qt = torch.from_numpy(q).cuda()
-    out = F.compensated_attention(qt, kb, kr, vb, vr, B, H, S, d, kv_stride=stride)
-    # oracle on the first S positions of every (b, h)
+    out = F.compensated_attention(qt, kb, kr, vb, vr, B, H, S, d, kv_stride=stride, n_kv_heads=Hkv)
+    # oracle on the first S positions of every (b, kv head)
     ks, vs = k[:, :, :S], v[:, :, :S]
     Kb, Kr = O.encode_fused(ks.reshape(-1, d))
     Vb, Vr = O.encode_fused(vs.reshape(-1, d))
-    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, H, S, return_f32=True)
+    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, H, S, n_kv_heads=Hkv, return_f32=True)
     close(to_np(out).astype(np.float32), ref, what="stride")
-    z = F.compensated_attention(qt, kb, kr, vb, vr, B, H, 0, d, kv_stride=stride)
+    z = F.compensated_attention(qt, kb, kr, vb, vr, B, H, 0, d, kv_stride=stride, n_kv_heads=Hkv)
     assert torch.count_nonzero(z) == 0
 
 
