@@ -7,12 +7,15 @@
 // (LDS histograms flushed with atomics), and a one-block scan per (b, head)
 // picks the digit where the running count from the top reaches k.  After the
 // third pass the threshold T and the number `need` of keys equal to T that
-// are still to be taken are exact.  Ties at T are taken in key order: a
-// per-64-key-tile count of ties is prefix-summed, and the attention kernel
-// ranks ties inside a tile with a ballot.
+// are still to be taken are exact.  Ties at T are taken in key order, i.e.
+// up to a cutoff key index: the third pass also keeps each key chunk's
+// histogram, which locates the chunk holding the need-th tie; one block per
+// (b, head) then scans only that chunk for the cutoff index.  The attention
+// kernel selects key > T, or key == T at an index <= cutoff.
 //
-// Workspace: hist [B*Hq][2048] u32 | state [B*Hq] (prefix u32, remaining i32)
-//            | ties [B*Hq][n_tiles] i32 | attention partials.
+// Workspace: hist [B*Hq][2048] u32 | prefix [B*Hq] u32 | remain [B*Hq] i32
+//            | cutoff [B*Hq] i32 | chunk histograms [B*Hq][nsplit][1024] u32
+//            | attention partials.
 #include "common.h"
 
 namespace bc {
@@ -20,7 +23,7 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* need, const int32_t* tie_prefix, uint8_t* selected);
+                  const int32_t* cutoff, uint8_t* selected);
 size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
 }  // namespace bc
 
@@ -31,11 +34,13 @@ constexpr int kBins = 2048;
 struct SelArgs {
     const uint16_t* q;
     BinPlanes kb;
-    int Hq, Hkv, S, kv_stride, n_tiles;
+    int Hq, Hkv, S, kv_stride;
+    int nsplit, chunk;   // key chunks of the histogram passes
     uint32_t* hist;      // [B*Hq][2048]
     uint32_t* prefix;    // [B*Hq]
     int32_t* remain;     // [B*Hq]
-    int32_t* ties;       // [B*Hq][n_tiles]
+    int32_t* cutoff;     // [B*Hq]
+    uint32_t* chist;     // [B*Hq][nsplit][1024] last-pass histogram of each chunk
 };
 
 template <int D, int G>
@@ -92,6 +97,8 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
         const uint32_t c = (&h[0][0])[i];
         const int g = i / kBins, bin = i % kBins;
         if (c) atomicAdd(&a.hist[(int64_t)(bhq0 + g) * kBins + bin], c);
+        if (pass == 2 && bin < 1024)
+            a.chist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * 1024 + bin] = c;
     }
 }
 
@@ -155,60 +162,67 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_
     }
 }
 
-// Ties at the final threshold per 64-key tile.
-template <int D, int G>
-__global__ __launch_bounds__(256) void tie_count_kernel(SelArgs a, int chunk) {
-    __shared__ uint32_t qs[G][D / 32];
-    const int nqg = (a.Hq / a.Hkv) / G;
-    const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
-    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-    const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
-    load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
-    __syncthreads();
-    const int64_t base = (int64_t)bkv * a.kv_stride;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
-    for (int t0 = k0 + wave * 64; t0 < k1; t0 += 256) {
-        const int s = t0 + lane;
-        const bool valid = s < k1;
-        const int64_t vi = base + (valid ? s : t0);
-        const SignWords<D> ks = load_signs<D>(a.kb.signs + vi * (D / 8));
-        const float sk = h2f(a.kb.scales[vi]);
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const uint32_t T = a.prefix[bhq0 + g];
-            const bool tie = valid && key_of<D>(qs[g], ks, sk) == T;
-            const uint64_t m = __ballot(tie);
-            if (lane == 0) a.ties[(int64_t)(bhq0 + g) * a.n_tiles + (t0 >> 6)] = __builtin_popcountll(m);
-        }
+// Cutoff index of the ties at the final threshold T: one block per (b, query
+// head).  The chunk histograms give the chunk holding the need-th tie; that
+// chunk is scanned in key order, 256 keys at a time.
+template <int D>
+__global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
+    __shared__ uint32_t qs[1][D / 32];
+    __shared__ int sh_chunk, sh_rank;
+    __shared__ int wcount[4];
+    const int bhq = blockIdx.x;
+    const int b = bhq / a.Hq, h = bhq % a.Hq;
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int need = a.remain[bhq];
+    if (need <= 0) {
+        if (threadIdx.x == 0) a.cutoff[bhq] = -1;
+        return;
     }
-}
-
-// Exclusive prefix over tiles, one block per (b, query head).
-__global__ __launch_bounds__(256) void tie_scan_kernel(int32_t* ties, int n_tiles) {
-    __shared__ int32_t part[256];
-    int32_t* t = ties + (int64_t)blockIdx.x * n_tiles;
-    const int per = (n_tiles + 255) / 256;
-    const int lo = threadIdx.x * per, hi = min(n_tiles, lo + per);
-    int32_t sum = 0;
-    for (int i = lo; i < hi; i++) sum += t[i];
-    part[threadIdx.x] = sum;
-    __syncthreads();
+    const uint32_t T = a.prefix[bhq];
+    load_q_signs<D, 1>(a.q + (int64_t)bhq * D, qs);
     if (threadIdx.x == 0) {
-        int32_t run = 0;
-        for (int i = 0; i < 256; i++) {
-            const int32_t v = part[i];
-            part[i] = run;
-            run += v;
+        const uint32_t* ch = a.chist + (int64_t)bhq * a.nsplit * 1024 + (T & 0x3FFu);
+        int cum = 0, c = 0;
+        for (; c < a.nsplit - 1; c++) {
+            const int t = (int)ch[(int64_t)c * 1024];
+            if (cum + t >= need) break;
+            cum += t;
         }
+        sh_chunk = c;
+        sh_rank = need - cum;   // the rank-th tie (from 1) of chunk c is the last one taken
     }
     __syncthreads();
-    int32_t run = part[threadIdx.x];
-    for (int i = lo; i < hi; i++) {
-        const int32_t v = t[i];
-        t[i] = run;
-        run += v;
+    const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
+    const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int rank = sh_rank;
+    int found = -1;
+    for (int s0 = k0; s0 < k1; s0 += 256) {
+        const int s = s0 + threadIdx.x;
+        bool tie = false;
+        if (s < k1) {
+            const SignWords<D> ks = load_signs<D>(a.kb.signs + (base + s) * (D / 8));
+            tie = key_of<D>(qs[0], ks, h2f(a.kb.scales[base + s])) == T;
+        }
+        const uint64_t m = __ballot(tie);
+        if (lane == 0) wcount[wave] = __builtin_popcountll(m);
+        __syncthreads();
+        int before = 0, total = 0;
+        for (int w = 0; w < 4; w++) {
+            if (w < wave) before += wcount[w];
+            total += wcount[w];
+        }
+        if (rank <= total) {
+            // the rank-th tie is in this block of keys
+            const int mine = before + __builtin_popcountll(m & ((1ull << lane) - 1ull)) + 1;
+            if (tie && mine == rank) found = s;
+            break;
+        }
+        rank -= total;
+        __syncthreads();
     }
+    // exactly one thread found it (rank <= ties in the chunk by construction)
+    if (found >= 0) a.cutoff[bhq] = found;
 }
 
 __global__ void zero_kernel(uint32_t* p, int64_t n) {
@@ -223,20 +237,41 @@ int pick_g(int group) {
     return 1;
 }
 
+struct Chunks {
+    int nsplit, chunk;
+};
+
+// key chunks of the histogram passes: ~4 workgroups per CU over all groups
+Chunks chunks_for(int batch, int hq, int hkv, int S) {
+    const int G = pick_g(hq / hkv);
+    const int groups = batch * hkv * ((hq / hkv) / G);
+    const int tiles = (S + 63) / 64;
+    int nsplit = (4 * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
+    if (nsplit > tiles) nsplit = tiles;
+    if (nsplit < 1) nsplit = 1;
+    const int tiles_per = (tiles + nsplit - 1) / nsplit > 0 ? (tiles + nsplit - 1) / nsplit : 1;
+    Chunks c;
+    c.chunk = tiles_per * 64;
+    c.nsplit = (tiles + tiles_per - 1) / tiles_per;
+    if (c.nsplit < 1) c.nsplit = 1;
+    return c;
+}
+
 struct Layout {
-    size_t hist, prefix, remain, ties, attn, total;
+    size_t hist, prefix, remain, cutoff, chist, attn, total;
 };
 
 Layout layout(int batch, int hq, int hkv, int S, int d) {
     Layout L;
     const size_t bh = (size_t)batch * hq;
-    const size_t n_tiles = (size_t)(S + 63) / 64;
+    const Chunks c = chunks_for(batch, hq, hkv, S);
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.hist = 0;
     L.prefix = al(L.hist + bh * kBins * 4);
     L.remain = al(L.prefix + bh * 4);
-    L.ties = al(L.remain + bh * 4);
-    L.attn = al(L.ties + bh * (n_tiles ? n_tiles : 1) * 4);
+    L.cutoff = al(L.remain + bh * 4);
+    L.chist = al(L.cutoff + bh * 4);
+    L.attn = al(L.chist + bh * (size_t)c.nsplit * 1024 * 4);
     L.total = L.attn + bc::attention_ws_bytes(batch, hq, hkv, S, d);
     return L;
 }
@@ -249,8 +284,7 @@ void run_passes(const SelArgs& a, int splits_y, int chunk, int nsplit, int bh, i
         hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a, pass, chunk);
         hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, pass, top_k);
     }
-    hipLaunchKernelGGL((tie_count_kernel<D, G>), grid, dim3(256), 0, st, a, chunk);
-    hipLaunchKernelGGL(tie_scan_kernel, dim3(bh), dim3(256), 0, st, a.ties, a.n_tiles);
+    hipLaunchKernelGGL((tie_locate_kernel<D>), dim3(bh), dim3(256), 0, st, a);
 }
 
 template <int D>
@@ -304,25 +338,21 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     a.Hkv = n_kv_heads;
     a.S = seq_len;
     a.kv_stride = kv_stride;
-    a.n_tiles = (seq_len + 63) / 64;
     a.hist = (uint32_t*)(ws + L.hist);
     a.prefix = (uint32_t*)(ws + L.prefix);
     a.remain = (int32_t*)(ws + L.remain);
-    a.ties = (int32_t*)(ws + L.ties);
+    a.cutoff = (int32_t*)(ws + L.cutoff);
+    a.chist = (uint32_t*)(ws + L.chist);
     // clear the histograms with a kernel (no memset nodes: graph-capture safe)
     hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, a.hist, (int64_t)bh * kBins);
     int rc = bc::check_launch("adaptive zero");
     if (rc != BC_OK) return rc;
     const int G = pick_g(n_heads / n_kv_heads);
     const int groups = batch * n_kv_heads * ((n_heads / n_kv_heads) / G);
-    const int tiles = a.n_tiles;
-    int nsplit = (4 * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
-    if (nsplit > tiles) nsplit = tiles;
-    if (nsplit < 1) nsplit = 1;
-    const int tiles_per = (tiles + nsplit - 1) / nsplit > 0 ? (tiles + nsplit - 1) / nsplit : 1;
-    const int chunk = tiles_per * 64;
-    nsplit = (tiles + tiles_per - 1) / tiles_per;
-    if (nsplit < 1) nsplit = 1;
+    const Chunks c = chunks_for(batch, n_heads, n_kv_heads, seq_len);
+    const int nsplit = c.nsplit, chunk = c.chunk;
+    a.nsplit = nsplit;
+    a.chunk = chunk;
     const int k = top_k > seq_len ? seq_len : top_k;
     switch (head_dim) {
         case 32: run_passes_g<32>(G, a, groups, chunk, nsplit, bh, k, st); break;
@@ -339,5 +369,5 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     if (rc != BC_OK) return rc;
     return bc::run_attention(2, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
                              seq_len, kv_stride, head_dim, ws + L.attn, workspace_bytes - L.attn,
-                             st, a.prefix, a.remain, a.ties, selected);
+                             st, a.prefix, a.cutoff, selected);
 }

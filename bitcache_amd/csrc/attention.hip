@@ -147,12 +147,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     }
 
     uint32_t thresh[G];
-    int need[G];
+    int cutoff[G];
     if constexpr (MODE == MODE_ADAPTIVE) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             thresh[g] = a.thresh[bhq0 + g];
-            need[g] = a.need[bhq0 + g];
+            cutoff[g] = a.cutoff[bhq0 + g];
         }
     }
 
@@ -205,15 +205,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             // (scale_q * scale_k) * (2pc - d)   (src/xnor_dot.cuh:179)
             const float xdot = (qp[g].scale_q * sk) * mq;
             if constexpr (MODE == MODE_ADAPTIVE) {
+                // above the threshold, or equal to it up to the cutoff index
                 const uint32_t key = ordered_key(sk * mq);
-                const uint64_t tie = __ballot(valid && key == thresh[g]);
-                bool sel = key > thresh[g];
-                if (key == thresh[g] && need[g] > 0) {
-                    // rank of this tie among all ties of the key range, in key order
-                    const int before = __builtin_popcountll(tie & ((1ull << lane) - 1ull));
-                    const int tile = t0 >> 6;
-                    sel = (a.tie_prefix[(int64_t)(bhq0 + g) * a.n_tiles + tile] + before) < need[g];
-                }
+                const bool sel = key > thresh[g] || (key == thresh[g] && s <= cutoff[g]);
                 selmask |= (sel && valid) ? (1u << g) : 0u;
             }
             sc[g] = xdot;
@@ -806,8 +800,8 @@ namespace bc {
 int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
                 const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
-                hipStream_t st, const uint32_t* thresh, const int32_t* need,
-                const int32_t* tie_prefix, uint8_t* selected) {
+                hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
+                uint8_t* selected) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -834,9 +828,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.chunk = p.chunk;
     a.ws = (float*)workspace;
     a.thresh = thresh;
-    a.need = need;
-    a.tie_prefix = tie_prefix;
-    a.n_tiles = (seq_len + 63) / 64;
+    a.cutoff = cutoff;
     a.selected = selected;
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     // matrix-core value phase for head_dim 64/128/256; the VALU kernel covers the
@@ -867,10 +859,10 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* need, const int32_t* tie_prefix, uint8_t* selected) {
+                  const int32_t* cutoff, uint8_t* selected) {
     int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
-                         kv_stride, head_dim, workspace, workspace_bytes, st, thresh, need,
-                         tie_prefix, selected);
+                         kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
+                         selected);
     if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
@@ -900,8 +892,7 @@ extern "C" int bc_attention_partial(const void* q, const void* k_bin, const void
                "k_res and v_res must both be given or both be null");
     return bc::run_partial(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, batch,
                            n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
-                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr,
-                           nullptr);
+                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads,
@@ -915,7 +906,7 @@ extern "C" int bc_binary_attention(const void* q, const void* k_bin, const void*
                                    void* workspace, size_t workspace_bytes, void* stream) {
     return bc::run_attention(MODE_BINARY, q, k_bin, nullptr, v_bin, nullptr, out, batch, n_heads,
                              n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
-                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+                             (hipStream_t)stream, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_compensated_attention(const void* q, const void* k_bin, const void* k_res,
@@ -924,7 +915,7 @@ extern "C" int bc_compensated_attention(const void* q, const void* k_bin, const 
                                         size_t workspace_bytes, void* stream) {
     return bc::run_attention(MODE_COMP, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads,
                              n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
-                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+                             (hipStream_t)stream, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_res,
@@ -936,8 +927,7 @@ extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_
                "k_res and v_res must both be given or both be null");
     return bc::run_attention(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, out,
                              batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
-                             workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr,
-                             nullptr);
+                             workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
 }
 
 template <int D>

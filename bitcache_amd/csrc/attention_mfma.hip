@@ -228,7 +228,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // issued before the prefetch and never less.
     constexpr int kSignDma = SB >= 16 ? SB / 16 : 1;
     constexpr int kVDma = kSignDma + (MODE == MODE_COMP ? Q : 0);
-    constexpr int kKLoads = (SB + 15) / 16 + (MODE == MODE_COMP ? 4 + Q : 2);
+    constexpr int kKLoads = (SB + 15) / 16 + (RES ? 4 + Q : 2);
     constexpr int kPrefetchOps = kVDma + kKLoads;
     static_assert(kPrefetchOps + kVDma < 64, "vmcnt holds 6 bits");
     // GQA groups in compensated mode run without the one-tile prefetch: one
@@ -295,19 +295,19 @@ void attn_mfma_kernel(AttnArgs a) {
     bool have_wexp = false;
 
     uint32_t thresh[G];
-    int need[G];
+    int cutoff[G];
     if constexpr (MODE == MODE_ADAPTIVE) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             thresh[g] = a.thresh[bhq0 + g];
-            need[g] = a.need[bhq0 + g];
+            cutoff[g] = a.cutoff[bhq0 + g];
         }
     }
 
     // query digits of a single head in scalar registers for the whole loop
     // (uniform operands of v_dot8) when codes are read per key
-    int sdig[(G == 1 && MODE == MODE_COMP && !LIN_K) ? CW : 1][4];
-    if constexpr (G == 1 && MODE == MODE_COMP && !LIN_K) {
+    int sdig[(G == 1 && RES && !LIN_K) ? CW : 1][4];
+    if constexpr (G == 1 && RES && !LIN_K) {
 #pragma unroll
         for (int w = 0; w < CW; w++) {
             const int4 dg = qd.digits[0][w];
@@ -348,7 +348,10 @@ void attn_mfma_kernel(AttnArgs a) {
         r.svv = a.vb.scales[ki];
         r.rsk = 0;
         r.rsv = 0;
-        if constexpr (MODE == MODE_COMP) {
+        // residual scales and K codes of every key (adaptive mode too: the
+        // selection is known only after the scores, and these loads are the
+        // ones worth prefetching; V codes are gathered for selected keys)
+        if constexpr (RES) {
             r.rsk = a.kr.scales[ki];
             r.rsv = a.vr.scales[ki];
             if constexpr (KMF) {
@@ -427,7 +430,7 @@ void attn_mfma_kernel(AttnArgs a) {
         const float sk = h2f(r.sk), svv = h2f(r.svv);
         float rsk = h2f(r.rsk), rsv = h2f(r.rsv);
         uint32_t kc[CW];
-        if constexpr (MODE == MODE_COMP) {
+        if constexpr (RES) {
 #pragma unroll
             for (int w = 0; w < CW; w++) kc[w] = r.kc[w];
         }
@@ -442,28 +445,15 @@ void attn_mfma_kernel(AttnArgs a) {
             const float mq = (float)(2 * pc - D);
             xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:179)
             if constexpr (MODE == MODE_ADAPTIVE) {
+                // selected: above the threshold, or equal to it at an index up to
+                // the cutoff (ties are taken lowest index first)
                 const uint32_t key = ordered_key(sk * mq);
-                const uint64_t tie = __ballot(valid && key == thresh[g]);
-                bool sel = key > thresh[g];
-                if (key == thresh[g] && need[g] > 0) {
-                    const int before = __builtin_popcountll(tie & ((1ull << lane) - 1ull));
-                    sel = (a.tie_prefix[(int64_t)(bhq0 + g) * a.n_tiles + (t0 >> 6)] + before) < need[g];
-                }
+                const bool sel = key > thresh[g] || (key == thresh[g] && s <= cutoff[g]);
                 selmask |= (sel && valid) ? (1u << g) : 0u;
             }
         }
         if constexpr (MODE == MODE_ADAPTIVE) {
             if (selmask) {
-                rsk = h2f(a.kr.scales[ki]);
-                rsv = h2f(a.vr.scales[ki]);
-                if constexpr (!KMF) {
-                    const uint4* cp = (const uint4*)(a.kr.codes + ki * CB);
-#pragma unroll
-                    for (int i = 0; i < CW / 4; i++) {
-                        const uint4 c = cp[i];
-                        kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
-                    }
-                }
                 const uint8_t* vc = a.vr.codes + ki * CB;
 #pragma unroll
                 for (int c = 0; c < Q; c++)
@@ -475,25 +465,6 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
                 for (int g = 0; g < G; g++)
                     a.selected[(int64_t)(bhq0 + g) * a.S + s] = (selmask >> g) & 1u;
-            }
-            if constexpr (KMF) {
-                // code pieces (matrix-core layout) of the keys any head selected
-                const uint64_t anysel = __ballot(selmask != 0u);
-                if (anysel != 0ull) {
-#pragma unroll
-                    for (int kb = 0; kb < 4; kb++) {
-                        const int key = 16 * kb + (lane & 15);
-                        if ((anysel >> key) & 1ull) {
-                            const int64_t kk = kv_base + t0 + key;
-#pragma unroll
-                            for (int pc = 0; pc < NPC; pc++) {
-                                const uint4 c = *(const uint4*)(a.kr.codes + kk * CB + 16 * ((lane >> 4) + 4 * pc));
-                                const int i = kb * NPC + pc;
-                                kc[4 * i] = c.x; kc[4 * i + 1] = c.y; kc[4 * i + 2] = c.z; kc[4 * i + 3] = c.w;
-                            }
-                        }
-                    }
-                }
             }
         }
 
@@ -568,7 +539,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-        } else if constexpr (G == 1 && MODE == MODE_COMP) {
+        } else if constexpr (G == 1 && RES && !LIN_K) {
             {
                 int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll

@@ -19,9 +19,8 @@ struct AttnArgs {
     float* ws;            // [B*Hq][n_splits][D + 2]: m (log2 domain), l, acc[D]
     // adaptive selection (MODE_ADAPTIVE)
     const uint32_t* thresh;      // [B*Hq] ordered key threshold
-    const int32_t* need;         // [B*Hq] ties at the threshold still to take
-    const int32_t* tie_prefix;   // [B*Hq][n_tiles] ties in earlier 64-key tiles
-    int n_tiles;
+    const int32_t* cutoff;       // [B*Hq] keys equal to the threshold are taken up to
+                                 // this key index (-1: none)
     uint8_t* selected;           // optional [B, Hq, S]
 };
 
