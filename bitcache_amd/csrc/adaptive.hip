@@ -82,14 +82,27 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
     for (int g = 0; g < G; g++) pref[g] = pass == 0 ? 0u : a.prefix[bhq0 + g];
     const int64_t base = (int64_t)bkv * a.kv_stride;
     const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
-    for (int s = k0 + threadIdx.x; s < k1; s += blockDim.x) {
-        const SignWords<D> ks = load_signs<D>(a.kb.signs + (base + s) * (D / 8));
-        const float sk = h2f(a.kb.scales[base + s]);
+    // four keys per thread per iteration, all loads issued first
+    constexpr int U = 4;
+    for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
+        SignWords<D> ks[U];
+        float sk[U];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const uint32_t u = key_of<D>(qs[g], ks, sk);
-            const bool match = pbits == 0 || (u >> (32 - pbits)) == (pref[g] >> (32 - pbits));
-            if (match) atomicAdd(&h[g][(u >> shift) & dmask], 1u);
+        for (int u = 0; u < U; u++) {
+            const int ss = s + u * blockDim.x;
+            const int64_t i = base + (ss < k1 ? ss : s);
+            ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
+            sk[u] = h2f(a.kb.scales[i]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (s + u * (int)blockDim.x >= k1) break;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const uint32_t key = key_of<D>(qs[g], ks[u], sk[u]);
+                const bool match = pbits == 0 || (key >> (32 - pbits)) == (pref[g] >> (32 - pbits));
+                if (match) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+            }
         }
     }
     __syncthreads();
@@ -127,38 +140,43 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_
     }
     part[threadIdx.x] = local;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        if (remain <= 0) {
-            if (pass == 0) {
-                a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
-                a.remain[bhq] = 0;
-            }
-        } else {
-            uint32_t above = 0;
-            int t = 0;
-            for (; t < 256; t++) {
-                if (above + part[t] >= (uint32_t)remain) break;
-                above += part[t];
-            }
-            if (t == 256) {
-                // fewer matching keys than remain: select everything
-                a.prefix[bhq] = 0u;
-                a.remain[bhq] = 0;
-            } else {
-                int digit = 0;
-                for (int j = 0; j < per; j++) {
-                    const int d = nbins - 1 - (t * per + j);
-                    if (d < 0) break;
-                    if (above + cnt[d] >= (uint32_t)remain) {
-                        digit = d;
-                        break;
-                    }
-                    above += cnt[d];
-                }
-                a.prefix[bhq] = prefix | ((uint32_t)digit << shift);
-                a.remain[bhq] = remain - (int)above;
-            }
+    if (remain <= 0) {
+        if (threadIdx.x == 0 && pass == 0) {
+            a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
+            a.remain[bhq] = 0;
         }
+        return;
+    }
+    // inclusive prefix over the 256 partial counts (Hillis-Steele in LDS)
+    uint32_t incl = local;
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
+        __syncthreads();
+        incl += add;
+        part[threadIdx.x] = incl;
+        __syncthreads();
+    }
+    const uint32_t excl = incl - local;
+    if (threadIdx.x == 255 && incl < (uint32_t)remain) {
+        // fewer matching keys than remain: select everything
+        a.prefix[bhq] = 0u;
+        a.remain[bhq] = 0;
+    }
+    if (excl < (uint32_t)remain && incl >= (uint32_t)remain) {
+        // this thread's 8 bins hold the remain-th largest key
+        uint32_t above = excl;
+        int digit = 0;
+        for (int j = 0; j < per; j++) {
+            const int d = nbins - 1 - (threadIdx.x * per + j);
+            if (d < 0) break;
+            if (above + cnt[d] >= (uint32_t)remain) {
+                digit = d;
+                break;
+            }
+            above += cnt[d];
+        }
+        a.prefix[bhq] = prefix | ((uint32_t)digit << shift);
+        a.remain[bhq] = remain - (int)above;
     }
 }
 
@@ -169,7 +187,7 @@ template <int D>
 __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     __shared__ uint32_t qs[1][D / 32];
     __shared__ int sh_chunk, sh_rank;
-    __shared__ int wcount[4];
+    __shared__ int wcount[4][4];
     const int bhq = blockIdx.x;
     const int b = bhq / a.Hq, h = bhq % a.Hq;
     const int kvh = h / (a.Hq / a.Hkv);
@@ -195,30 +213,49 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
     const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
     int rank = sh_rank;
     int found = -1;
-    for (int s0 = k0; s0 < k1; s0 += 256) {
-        const int s = s0 + threadIdx.x;
-        bool tie = false;
-        if (s < k1) {
-            const SignWords<D> ks = load_signs<D>(a.kb.signs + (base + s) * (D / 8));
-            tie = key_of<D>(qs[0], ks, h2f(a.kb.scales[base + s])) == T;
+    // 1024 keys per step (4 per thread, loads first); key order = u, wave, lane
+    for (int s0 = k0; s0 < k1; s0 += 1024) {
+        bool tie[4];
+        SignWords<D> ks[4];
+        float sk[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int s = s0 + u * 256 + (int)threadIdx.x;
+            const int64_t i = base + (s < k1 ? s : k0);
+            ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
+            sk[u] = h2f(a.kb.scales[i]);
         }
-        const uint64_t m = __ballot(tie);
-        if (lane == 0) wcount[wave] = __builtin_popcountll(m);
+        uint64_t m[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int s = s0 + u * 256 + (int)threadIdx.x;
+            tie[u] = s < k1 && key_of<D>(qs[0], ks[u], sk[u]) == T;
+            m[u] = __ballot(tie[u]);
+            if (lane == 0) wcount[u][wave] = __builtin_popcountll(m[u]);
+        }
         __syncthreads();
-        int before = 0, total = 0;
-        for (int w = 0; w < 4; w++) {
-            if (w < wave) before += wcount[w];
-            total += wcount[w];
+        bool done = false;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            int before = 0, total = 0;
+            for (int w = 0; w < 4; w++) {
+                if (w < wave) before += wcount[u][w];
+                total += wcount[u][w];
+            }
+            if (!done) {
+                if (rank <= total) {
+                    const int mine = before + __builtin_popcountll(m[u] & below) + 1;
+                    if (tie[u] && mine == rank) found = s0 + u * 256 + (int)threadIdx.x;
+                    done = true;
+                } else {
+                    rank -= total;
+                }
+            }
         }
-        if (rank <= total) {
-            // the rank-th tie is in this block of keys
-            const int mine = before + __builtin_popcountll(m & ((1ull << lane) - 1ull)) + 1;
-            if (tie && mine == rank) found = s;
-            break;
-        }
-        rank -= total;
+        if (done) break;
         __syncthreads();
     }
     // exactly one thread found it (rank <= ties in the chunk by construction)

@@ -176,6 +176,9 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_MHA_PIPE
 #define BC_MHA_PIPE 1
 #endif
+#ifndef BC_ADAPT_PIPE
+#define BC_ADAPT_PIPE 1
+#endif
 #ifndef BC_GQA_PIPE
 #define BC_GQA_PIPE 0
 #endif
@@ -187,7 +190,7 @@ struct Occupancy {
     static constexpr int kWaves =
         MODE == MODE_BINARY ? (D <= 128 ? (G <= 2 ? BC_BIN_WAVES : 3) : 2)
                             : ((G == 1 && D <= 128) ? BC_MHA_WAVES
-                                                    : (D <= 128 ? (G <= 4 && MODE == MODE_COMP && !BC_GQA_PIPE ? 3 : 2) : 1));
+                                                    : (D <= 128 ? (G <= 4 && !BC_GQA_PIPE && (MODE == MODE_COMP || !BC_ADAPT_PIPE) ? 3 : 2) : 1));
 };
 
 // Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
@@ -234,7 +237,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // GQA groups in compensated mode run without the one-tile prefetch: one
     // staging buffer and one K register set leave room for a third workgroup
     // per CU (measured faster); adaptive mode keeps it
-    constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || MODE == MODE_ADAPTIVE || BC_GQA_PIPE;
+    constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || (MODE == MODE_ADAPTIVE && BC_ADAPT_PIPE) || BC_GQA_PIPE;
     using WL = WaveLds<D, G, RES, PIPE ? 2 : 1>;
 
     __shared__ QDigits<D, G> qd;
