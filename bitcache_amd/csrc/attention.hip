@@ -715,19 +715,23 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
     const int tiles = (S + 63) / 64;
     const int cu = bc::device_cu_count();
     // ~8 workgroups per CU: several rounds of 2-3 resident workgroups per CU keep
-    // the tail of the launch short (measured on the 64K-context MHA step)
+    // the tail of the launch short (measured on the 64K-context MHA step).  A
+    // launch too small for two such rounds instead fills exactly one round of
+    // 3 workgroups per CU (measured on the 16K-context GQA decode step).
     int want = (8 * cu + groups - 1) / groups;
+    int max_split = tiles / 8;                   // at least 8 tiles (2 per wave) per split
+    if (max_split < 1) max_split = 1;
+    if (want > max_split) want = max_split;
+    if ((int64_t)groups * want < 6LL * cu) {
+        const int one_round = (3 * cu) / (groups > 0 ? groups : 1);
+        want = one_round < max_split ? one_round : max_split;
+    }
     static const int forced = [] {
         const char* e = getenv("BITCACHE_SPLITS");
         return e ? atoi(e) : 0;
     }();
-    if (forced > 0) want = forced;
+    if (forced > 0) want = forced < tiles ? forced : tiles;   // tuning override
     if (want > kMaxSplits) want = kMaxSplits;   // the combine kernel's weight table
-    // at least 16 tiles (4 per wave) per split: the per-workgroup query set-up
-    // is amortised (measured on the 16K-context GQA decode step)
-    int max_split = tiles / 16;
-    if (max_split < 1) max_split = 1;
-    if (want > max_split) want = max_split;
     if (want < 1) want = 1;
     const int tiles_per = (tiles + want - 1) / want;
     p.chunk = tiles_per * 64;
