@@ -274,11 +274,18 @@ void attn_mfma_kernel(AttnArgs a) {
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
     const int my_head = my_col >> 1;
+    const int bcol = my_col < 2 * G ? my_col : (my_col & 1);
 
-    float m[G], lsum[G], off[G];
+    // softmax reference per head, lowered lazily: weights p = 2^(s - m) stay
+    // <= 2^kTau, and the accumulators are rescaled only when a score passes
+    // m + kTau (the result does not depend on m)
+    constexpr int kTauI = 8;
+    constexpr float kTau = (float)kTauI;
+    float m[G], mlim[G], lsum[G], off[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         m[g] = -INFINITY;
+        mlim[g] = -INFINITY;
         lsum[g] = 0.0f;
         off[g] = 0.0f;
     }
@@ -292,10 +299,12 @@ void attn_mfma_kernel(AttnArgs a) {
     for (int d = 0; d < NB; d++) cn[d] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     // weights enter the MFMAs as w * 2^wexp (fp16 hi + lo), wexp chosen so the
-    // largest weight sits near 2^14: no overflow, and weights down to ~2^-38 of
-    // the largest keep their contribution (undone exactly in the epilogue)
+    // largest possible weight sits near 2^14: no overflow, and weights down to
+    // ~2^-30 of the largest keep their contribution (undone exactly in the
+    // epilogue)
     int wexp = 0;
     bool have_wexp = false;
+    float wlim = 0.0f;
 
     uint32_t thresh[G];
     int cutoff[G];
@@ -480,8 +489,9 @@ void attn_mfma_kernel(AttnArgs a) {
           if constexpr (MODE == MODE_ADAPTIVE) kmf_run = __ballot(selmask != 0u) != 0ull;
           if (kmf_run) {
             // codes as int8 16*n (signed): low nibbles via x << 4, high nibbles in
-            // place; each half of a piece is one 16x16x64 MFMA with 16 keys x 64 dims
-            // (rows of keys whose codes were not loaded are never used)
+            // place; each half of a piece is one 16x16x64 MFMA of (head, digit
+            // plane) rows x 64 dims times 64 dims x 16 keys (columns of keys whose
+            // codes were not loaded are never used)
             v4i_t acc[4];
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
@@ -494,28 +504,32 @@ void attn_mfma_kernel(AttnArgs a) {
                         const uint32_t x1 = kc[4 * (kb * NPC + pc) + 2 * h + 1];
                         const v4i_t av = v4i_t{(int)((x0 << 4) & 0xF0F0F0F0u), (int)(x0 & 0xF0F0F0F0u),
                                                (int)((x1 << 4) & 0xF0F0F0F0u), (int)(x1 & 0xF0F0F0F0u)};
-                        acc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq[pc][h], acc[kb], 0, 0, 0);
+                        acc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bq[pc][h], av, acc[kb], 0, 0, 0);
                     }
             }
-            // lane l holds keys 16kb + 4(l/16) + i, column l%16 = (head, plane):
-            // planes of a head are neighbouring lanes -> q_int dot * 16 on even lanes
+            // lane l holds rows 4(l/16) + i = (head 2(l/16) + i/2, plane i%2) of
+            // key 16kb + l%16: both planes of a head sit in one lane, and
+            // q_int dot * 16 = plane0 + 256 plane1 goes to rdl[key][head]
+            if (lane < 8 * G) {
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                int v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int hi = __builtin_amdgcn_mov_dpp(acc[kb][i], 0xB1, 0xF, 0xF, true);
-                    v[i] = acc[kb][i] + hi * 256;
-                }
-                const int col = lane & 15;
-                if ((col & 1) == 0 && col < 2 * G)
-                    *(int4*)&rdl[(col >> 1) * 64 + 16 * kb + 4 * g4] = make_int4(v[0], v[1], v[2], v[3]);
+                for (int kb = 0; kb < 4; kb++)
+                    *(int2*)&rdl[(16 * kb + lj) * G + 2 * g4] =
+                        make_int2(acc[kb][0] + 256 * acc[kb][1], acc[kb][2] + 256 * acc[kb][3]);
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            // kept x16: the factor is folded into the score's scale below
+            if constexpr (G % 4 == 0) {
 #pragma unroll
-            for (int g = 0; g < G; g++) racc[g] = rdl[g * 64 + lane] >> 4;
+                for (int g = 0; g < G; g += 4) {
+                    const int4 v = *(const int4*)&rdl[lane * G + g];
+                    racc[g] = v.x; racc[g + 1] = v.y; racc[g + 2] = v.z; racc[g + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; g++) racc[g] = rdl[lane * G + g];
+            }
           }
         } else if constexpr (LIN_K) {
             // round i: this lane holds 32 dims (quarter) of key i*(64/Q) + l/Q;
@@ -586,31 +600,36 @@ void attn_mfma_kernel(AttnArgs a) {
             float score = xd[g];
             bool use_res = MODE == MODE_COMP;
             if constexpr (MODE == MODE_ADAPTIVE) use_res = (selmask >> g) & 1u;
-            if (RES && use_res) score = score + (float)racc[g] * (qd.dq[g] * (rsk * (1.0f / 7.0f)));
+            // (the matrix-core dots come x16, an exact power of two)
+            if (RES && use_res)
+                score = score + (float)racc[g] * (qd.dq[g] * (rsk * (KMF ? 1.0f / 112.0f : 1.0f / 7.0f)));
             sc[g] = valid ? score * isd2 : -INFINITY;
         }
 
-        // weight scale for this tile (p <= 1, so w <= max(2 sv, rs/7))
+        // weight scale: weights are p * wb * 2^wexp with p <= 2^kTau, so the
+        // plan holds while every wb <= wlim = 2^(14 - kTau - wexp); it is redone
+        // (one wave max) only when a key exceeds it, and then only lowered
         {
-            float wb = valid ? fmaxf(2.0f * svv, rsv * (1.0f / 7.0f)) : 0.0f;
-            wb = wave_max(wb);
-            if (wb > 0.0f && wb < INFINITY) {
-                const int e = 14 - (int)ceilf(log2f(wb));
-                if (!have_wexp) {
+            const float wb = valid ? fmaxf(2.0f * svv, rsv * (1.0f / 7.0f)) : 0.0f;
+            if (__ballot(wb > wlim) != 0ull) {
+                const float wmx = wave_max(wb);
+                if (wmx < INFINITY) {
+                    const int e = 14 - kTauI - (int)ceilf(log2f(wmx));
+                    if (have_wexp) {
+                        // a larger weight than planned (e < wexp): bring the sums down
+                        const float f = ldexpf(1.0f, e - wexp);
+#pragma unroll
+                        for (int h = 0; h < NH; h++)
+#pragma unroll
+                            for (int p = 0; p < 4; p++) cs[h][p] *= f;
+#pragma unroll
+                        for (int d = 0; d < NB; d++) cn[d] *= f;
+#pragma unroll
+                        for (int g = 0; g < G; g++) off[g] *= f;
+                    }
                     wexp = e;
                     have_wexp = true;
-                } else if (e < wexp) {
-                    // a larger weight than planned: bring the accumulated sums down
-                    const float f = ldexpf(1.0f, e - wexp);
-#pragma unroll
-                    for (int h = 0; h < NH; h++)
-#pragma unroll
-                        for (int p = 0; p < 4; p++) cs[h][p] *= f;
-#pragma unroll
-                    for (int d = 0; d < NB; d++) cn[d] *= f;
-#pragma unroll
-                    for (int g = 0; g < G; g++) off[g] *= f;
-                    wexp = e;
+                    wlim = ldexpf(1.0f, 14 - kTauI - wexp);
                 }
             }
         }
@@ -622,32 +641,45 @@ void attn_mfma_kernel(AttnArgs a) {
         // the value operands of odd keys come out 16x larger (see the MFMA
         // loops below): their weights carry 1/16 so that every product is exact
         const float kfac = (kown & 1) ? 0.0625f : 1.0f;
-        const float kinv = (kown & 1) ? 16.0f : 1.0f;
+        // per-key factors shared by the heads: sign weight a2 = p * fa, residual
+        // weight b = p * fb, and the offset sum_s (a_s + 8 b_s) grows by p * fo
+        const float fa = ldexpf(2.0f * svv * kfac, wexp);
+        const float fb = RES ? ldexpf(rsv * (1.0f / 7.0f) * kfac, wexp) : 0.0f;
+        const float fo_bin = ldexpf(svv, wexp);
+        const float fo_res = RES ? ldexpf(svv + rsv * (8.0f / 7.0f), wexp) : fo_bin;
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float mt = wave_max(sc[g]);
-            const float mn = fmaxf(m[g], mt);
-            if (mn > m[g]) {
-                const float alpha = exp2f(m[g] - mn);
+            // the reference m[g] moves only when a score passes m[g] + kTau
+            if (__ballot(sc[g] > mlim[g]) != 0ull) {
+                const float mn = fmaxf(m[g], wave_max(sc[g]));
+                const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);   // 0 when m was -inf
                 lsum[g] *= alpha;
                 off[g] *= alpha;
                 if (my_head == g) lane_alpha = alpha;
                 any_rescale = true;
                 m[g] = mn;
+                mlim[g] = mn + kTau;
             }
-            const float p = valid ? exp2f(sc[g] - mn) : 0.0f;
+            const float p = valid ? __builtin_amdgcn_exp2f(sc[g] - m[g]) : 0.0f;
             lsum[g] += p;
-            const float a2 = ldexpf(2.0f * p * svv * kfac, wexp);
-            float bv = 0.0f;
-            if constexpr (MODE == MODE_COMP) bv = ldexpf(p * (rsv * (1.0f / 7.0f)) * kfac, wexp);
-            if constexpr (MODE == MODE_ADAPTIVE)
-                bv = ((selmask >> g) & 1u) ? ldexpf(p * (rsv * (1.0f / 7.0f)) * kfac, wexp) : 0.0f;
+            const float a2 = p * fa;
+            float bv = 0.0f, fo = fo_bin;
+            if constexpr (MODE == MODE_COMP) {
+                bv = p * fb;
+                fo = fo_res;
+            }
+            if constexpr (MODE == MODE_ADAPTIVE) {
+                const bool selg = (selmask >> g) & 1u;
+                bv = selg ? p * fb : 0.0f;
+                fo = selg ? fo_res : fo_bin;
+            }
             const uint16_t a2h = f2h_bits(a2);
             const uint16_t a2l = f2h_bits(a2 - h_bits2f(a2h));
             const uint16_t bh = f2h_bits(bv);
             const uint16_t bl = f2h_bits(bv - h_bits2f(bh));
-            // offset removed at the end: sum_s (a_s + 8 b_s) with the weights as rounded
-            off[g] += kinv * (0.5f * (h_bits2f(a2h) + h_bits2f(a2l)) + 8.0f * (h_bits2f(bh) + h_bits2f(bl)));
+            // offset removed at the end, from the unrounded weights: the (hi, lo)
+            // pairs carry ~22 bits, so the difference is a zero-mean ~2^-22 term
+            off[g] = fmaf(p, fo, off[g]);
             wts[(0 * 2 * G + 2 * g) * 64 + sl] = a2h;
             wts[(0 * 2 * G + 2 * g + 1) * 64 + sl] = a2l;
             if constexpr (RES) {
@@ -678,18 +710,14 @@ void attn_mfma_kernel(AttnArgs a) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 
-        // B operands: (hi, lo) weight columns; unused columns are zero
+        // B operands: (hi, lo) weight columns; lanes of unused columns read
+        // columns 0/1 again (their output columns are never read back)
         h8_t bsig[2], bres[2];
 #pragma unroll
         for (int mh = 0; mh < 2; mh++) {
-            if (my_col < 2 * G) {
-                bsig[mh] = *(const h8_t*)&wts[(0 * 2 * G + my_col) * 64 + 16 * g4 + 8 * mh];
-                if constexpr (RES) bres[mh] = *(const h8_t*)&wts[(1 * 2 * G + my_col) * 64 + 16 * g4 + 8 * mh];
-                else bres[mh] = bsig[mh];
-            } else {
-                bsig[mh] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
-                bres[mh] = bsig[mh];
-            }
+            bsig[mh] = *(const h8_t*)&wts[(0 * 2 * G + bcol) * 64 + 16 * g4 + 8 * mh];
+            if constexpr (RES) bres[mh] = *(const h8_t*)&wts[(1 * 2 * G + bcol) * 64 + 16 * g4 + 8 * mh];
+            else bres[mh] = bsig[mh];
         }
 
         // all transposed reads of the tile first (they retire in order while
