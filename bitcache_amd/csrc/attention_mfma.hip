@@ -11,7 +11,7 @@
 //
 // Value phase: out[e] = sum_s a_s*(2*bit_se - 1) + b_s*(u_se - 8) with
 // a = p*sv, b = p*rs/7, u = n + 8.  The V tile (sign bytes and code bytes of
-// 64 keys) is copied global->LDS with direct loads, then ds_read_b64_tr_b4
+// 64 keys) is copied to LDS with direct buffer loads, then ds_read_b64_tr_b4
 // transposes 16 keys x 16 nibbles per 16-lane group so that each lane holds
 // 16 keys of one dimension.  Nibbles (u) and sign bits become exact fp16
 // subnormals (value * 2^(j-24) for bit position j < 10) with one mask per
@@ -36,7 +36,34 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u_t __attribute__((ext_vector_type(2)));
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+// Word 3 of a gfx9 buffer resource for raw byte-addressed loads (32-bit data
+// format, no swizzle; with stride 0 a load past num_records returns zeros).
+constexpr int kBufWord3 = 0x00020000;
+
+// D/8 sign bytes at byte offset off of a buffer, as D/32 words.
+template <int D>
+__device__ __forceinline__ SignWords<D> buf_signs(__amdgpu_buffer_rsrc_t r, int off) {
+    SignWords<D> s;
+    if constexpr (D % 128 == 0) {
+#pragma unroll
+        for (int i = 0; i < D / 128; i++) {
+            const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+            s.w[4 * i + 0] = v[0]; s.w[4 * i + 1] = v[1]; s.w[4 * i + 2] = v[2]; s.w[4 * i + 3] = v[3];
+        }
+    } else {
+        static_assert(D % 64 == 0, "sign rows of 8-byte multiples");
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) {
+            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8 * i, 0, 0);
+            s.w[2 * i + 0] = v[0]; s.w[2 * i + 1] = v[1];
+        }
+    }
+    return s;
+}
 
 template <int D, int G>
 struct QDigits {
@@ -342,48 +369,53 @@ void attn_mfma_kernel(AttnArgs a) {
             }
     }
 
-    // byte offset of the 16-byte piece `off` of a tile row plane with `rb`
-    // bytes per key; pieces of keys past the range re-read key t0's row (in
-    // range; their weight is 0), so every lane issues the same loads and no
-    // branch surrounds a load (the compiler's wait counts stay exact)
-    auto piece = [&](int t0, int off_in_tile, int rb) -> int64_t {
-        const int k = t0 + off_in_tile / rb;
-        return k < key_end ? (kv_base + t0) * rb + off_in_tile : (kv_base + t0) * rb + off_in_tile % rb;
+    // Buffer resources over this workgroup's key range [key_begin, key_end)
+    // of each plane: offsets are 32-bit and tile-relative, and a load of a key
+    // past the range returns zeros (its weight is 0), so no lane clamps its
+    // address and every lane issues the same loads (the wait counts stay exact)
+    const int nk = max(key_end - key_begin, 0);   // (an empty split issues no loads)
+    auto rsrc = [&](const void* plane, int rb) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const uint8_t*)plane + (kv_base + key_begin) * rb), (short)0, nk * rb, kBufWord3);
     };
+    const __amdgpu_buffer_rsrc_t r_ks = rsrc(a.kb.signs, SB), r_vs = rsrc(a.vb.signs, SB);
+    const __amdgpu_buffer_rsrc_t r_ksc = rsrc(a.kb.scales, 2), r_vsc = rsrc(a.vb.scales, 2);
+    const __amdgpu_buffer_rsrc_t r_kc = rsrc(a.kr.codes, CB), r_vc = rsrc(a.vr.codes, CB);
+    const __amdgpu_buffer_rsrc_t r_krs = rsrc(a.kr.scales, 2), r_vrs = rsrc(a.vr.scales, 2);
 
     // ---------------- loads of one tile: K side into registers, V side to LDS
     auto load_k = [&](KRegs<D>& r, int t0) {
-        const int s = t0 + kown;
-        const int64_t ki = kv_base + (s < key_end ? s : t0);
-        r.ks = load_signs<D>(a.kb.signs + ki * SB);
-        r.sk = a.kb.scales[ki];
-        r.svv = a.vb.scales[ki];
+        const int tr = t0 - key_begin;      // tile offset in the range (keys)
+        const int kk = tr + kown;
+        r.ks = buf_signs<D>(r_ks, kk * SB);
+        r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
+        r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
         r.rsk = 0;
         r.rsv = 0;
         // residual scales and K codes of every key (adaptive mode too: the
         // selection is known only after the scores, and these loads are the
         // ones worth prefetching; V codes are gathered for selected keys)
         if constexpr (RES) {
-            r.rsk = a.kr.scales[ki];
-            r.rsv = a.vr.scales[ki];
+            r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, kk * 2, 0, 0);
+            r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, kk * 2, 0, 0);
             if constexpr (KMF) {
                 // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
+                const int base = (tr + (lane & 15)) * CB + 16 * (lane >> 4);
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                     for (int pc = 0; pc < NPC; pc++) {
-                        const int sk2 = t0 + 16 * kb + (lane & 15);
-                        const int64_t kk = kv_base + (sk2 < key_end ? sk2 : t0);
-                        const uint4 c = *(const uint4*)(a.kr.codes + kk * CB + 16 * ((lane >> 4) + 4 * pc));
+                        const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 16 * kb * CB + 64 * pc, 0, 0);
                         const int i = kb * NPC + pc;
-                        r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+                        r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
                     }
             } else {
+                // per key: the lane's own row; linear: piece i*1024 + 16l of the tile
+                const int base = LIN_K ? tr * CB + 16 * lane : kk * CB;
 #pragma unroll
                 for (int i = 0; i < Q; i++) {
-                    const uint4 c = *(const uint4*)(a.kr.codes + (LIN_K ? piece(t0, i * 1024 + 16 * lane, CB)
-                                                                        : ki * CB + 16 * i));
-                    r.kc[4 * i] = c.x; r.kc[4 * i + 1] = c.y; r.kc[4 * i + 2] = c.z; r.kc[4 * i + 3] = c.w;
+                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + (LIN_K ? i * 1024 : 16 * i), 0, 0);
+                    r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
                 }
             }
         }
@@ -391,34 +423,26 @@ void attn_mfma_kernel(AttnArgs a) {
     // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear)
     // or piece c at c*1024 + 16k (per key)
     auto issue_v = [&](int buf, int t0) {
+        const int tr = t0 - key_begin;
         uint8_t* st_codes = my + buf * WL::kStage;
         uint8_t* st_signs = st_codes + WL::kCodeBytes;
         if constexpr (SB >= 16) {
 #pragma unroll
             for (int c = 0; c < SB / 16; c++)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(a.vb.signs + piece(t0, c * 1024 + 16 * lane, SB)),
-                    LDS_PTR(void, st_signs + c * 1024), 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs + c * 1024), 16,
+                                                         tr * SB + 16 * lane + c * 1024, 0, 0, 0);
         } else {
             // 8-byte rows: one KiB load covers 128 rows, so lanes 32..63 repeat
-            // lanes 0..31 (into bytes 512..1023).  The second key of the blob's
-            // last pair reads the first 8 bytes of the scale plane that follows
-            // the signs (the host guarantees 4 entries), and gets weight 0.
-            const int k2 = t0 + 2 * (lane & 31);
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void*)(a.vb.signs +
-                                                                (kv_base + (k2 < key_end ? k2 : t0)) * SB),
-                LDS_PTR(void, st_signs), 16, 0, 0);
+            // lanes 0..31 (into bytes 512..1023)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs), 16,
+                                                     tr * SB + 16 * (lane & 31), 0, 0, 0);
         }
         if constexpr (MODE == MODE_COMP) {
-            const int s = t0 + lane;
-            const int64_t ki = kv_base + (s < key_end ? s : t0);
 #pragma unroll
             for (int c = 0; c < Q; c++)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(a.vr.codes + (LIN_V ? piece(t0, c * 1024 + 16 * lane, CB)
-                                                                                         : ki * CB + 16 * c)),
-                    LDS_PTR(void, st_codes + c * 1024), 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
+                    (LIN_V ? tr * CB + 16 * lane : (tr + lane) * CB) + (LIN_V ? c * 1024 : 16 * c), 0, 0, 0);
         }
     };
 
@@ -428,7 +452,6 @@ void attn_mfma_kernel(AttnArgs a) {
         uint8_t* st_signs = st_codes + WL::kCodeBytes;
         const int s = t0 + kown;
         const bool valid = s < key_end;
-        const int64_t ki = kv_base + (valid ? s : t0);
         // this tile's K registers: the younger operations are this tile's V
         // loads and the whole next-tile prefetch.  An explicit count keeps the
         // compiler from draining the queue (with direct-to-LDS loads pending it
@@ -466,12 +489,10 @@ void attn_mfma_kernel(AttnArgs a) {
         }
         if constexpr (MODE == MODE_ADAPTIVE) {
             if (selmask) {
-                const uint8_t* vc = a.vr.codes + ki * CB;
 #pragma unroll
                 for (int c = 0; c < Q; c++)
-                    __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void*)(vc + 16 * c),
-                        LDS_PTR(void, st_codes + c * 1024), 16, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
+                                                             (s - key_begin) * CB + 16 * c, 0, 0, 0);
             }
             if (a.selected != nullptr && valid) {
 #pragma unroll
@@ -922,9 +943,8 @@ void launch_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
 namespace bc {
 
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
-    // D = 64 copies sign rows in key pairs, reading up to 8 bytes past the last
-    // key's row into the scale plane: that plane holds 8 bytes from 4 entries
-    if (D == 64 && (int64_t)a.B * a.Hkv * a.kv_stride < 4) return false;
+    // buffer offsets inside one split's key range are 32-bit
+    if ((int64_t)a.chunk * (D / 2) + 4096 >= ((int64_t)1 << 31)) return false;
     switch (D) {
         case 64: launch_d<64>(mode, G, a, grid, st); return true;
         case 128: launch_d<128>(mode, G, a, grid, st); return true;
