@@ -592,38 +592,67 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
 }
 
 // ---------------------------------------------------------------- binary scores
-// One lane per key; exact fp32 score (scale_q*scale_k)*(2pc-d) * (1/sqrt(d)).
+// One workgroup per (key chunk, b, kv head, batch of up to kScoreHeads query
+// heads of the group): each key's sign row and scale are read once and scored
+// against every head of the batch, one lane per key, kScoreUnroll keys in
+// flight per lane.  Exact fp32 score (scale_q*scale_k)*(2pc-d) * (1/sqrt(d)).
+constexpr int kScoreHeads = 16;
+constexpr int kScoreUnroll = 4;
+
 template <int D>
 __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlanes kb, float* scores,
                                                     int32_t* pcs, int Hq, int Hkv, int S,
-                                                    int kv_stride) {
-    __shared__ uint32_t qs[D / 32];
-    __shared__ float sq;
-    const int bh = blockIdx.y;
-    const int b = bh / Hq, h = bh % Hq;
-    const int kvh = h / (Hq / Hkv);
-    const uint16_t* qb = q + (int64_t)bh * D;
-    if (threadIdx.x < D / 32) {
+                                                    int kv_stride, int chunk, int n_hb) {
+    constexpr int W = D / 32;
+    __shared__ float qf[kScoreHeads][D];
+    __shared__ uint32_t qs[kScoreHeads][W];
+    __shared__ float sq[kScoreHeads];
+    const int G = Hq / Hkv;
+    const int hb = blockIdx.y % n_hb, bkv = blockIdx.y / n_hb;
+    const int b = bkv / Hkv, kvh = bkv % Hkv;
+    const int h0 = kvh * G + hb * kScoreHeads;                 // first query head of the batch
+    const int nh = min(kScoreHeads, G - hb * kScoreHeads);
+    const uint16_t* qb = q + ((int64_t)b * Hq + h0) * D;
+    for (int i = threadIdx.x; i < nh * D; i += blockDim.x) qf[i / D][i % D] = h2f(qb[i]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nh * W; i += blockDim.x) {
+        const int h = i / W, w = i % W;
         uint32_t bits = 0;
-        for (int i = 0; i < 32; i++) bits |= (h2f(qb[32 * threadIdx.x + i]) >= 0.0f ? 1u : 0u) << i;
-        qs[threadIdx.x] = bits;
+        for (int j = 0; j < 32; j++) bits |= (qf[h][32 * w + j] >= 0.0f ? 1u : 0u) << j;
+        qs[h][w] = bits;
     }
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < nh) {
         float acc = 0.0f;
-        for (int i = 0; i < D; i++) acc += fabsf(h2f(qb[i]));  // sequential (src/compensated_attention.cu:65-67)
-        sq = acc / (float)D;
+        for (int i = 0; i < D; i++) acc += fabsf(qf[threadIdx.x][i]);  // sequential (src/compensated_attention.cu:65-67)
+        sq[threadIdx.x] = acc / (float)D;
     }
     __syncthreads();
     const float isd = 1.0f / sqrtf((float)D);
-    const int64_t base = (int64_t)(b * Hkv + kvh) * kv_stride;
-    for (int s = blockIdx.x * blockDim.x + threadIdx.x; s < S; s += gridDim.x * blockDim.x) {
-        const SignWords<D> ks = load_signs<D>(kb.signs + (base + s) * (D / 8));
-        int pc = 0;
+    const int64_t base = (int64_t)bkv * kv_stride;
+    const int k0 = blockIdx.x * chunk, k1 = min(S, k0 + chunk);
+    for (int s0 = k0; s0 < k1; s0 += kScoreUnroll * 256) {
+        SignWords<D> ks[kScoreUnroll];
+        float sk[kScoreUnroll];
 #pragma unroll
-        for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
-        const float xdot = (sq * h2f(kb.scales[base + s])) * (float)(2 * pc - D);
-        if (scores) scores[(int64_t)bh * S + s] = xdot * isd;
-        if (pcs) pcs[(int64_t)bh * S + s] = pc;
+        for (int u = 0; u < kScoreUnroll; u++) {
+            const int s = s0 + u * 256 + (int)threadIdx.x;
+            const int64_t ki = base + (s < k1 ? s : k0);        // in range; unused past k1
+            ks[u] = load_signs<D>(kb.signs + ki * (D / 8));
+            sk[u] = h2f(kb.scales[ki]);
+        }
+#pragma unroll
+        for (int u = 0; u < kScoreUnroll; u++) {
+            const int s = s0 + u * 256 + (int)threadIdx.x;
+            if (s >= k1) continue;
+            for (int h = 0; h < nh; h++) {
+                int pc = 0;
+#pragma unroll
+                for (int w = 0; w < W; w++) pc += __builtin_popcount(~(qs[h][w] ^ ks[u].w[w]));
+                const int64_t o = ((int64_t)b * Hq + h0 + h) * S + s;
+                if (scores) scores[o] = ((sq[h] * sk[u]) * (float)(2 * pc - D)) * isd;
+                if (pcs) pcs[o] = pc;
+            }
+        }
     }
 }
 
@@ -937,9 +966,15 @@ extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_
 template <int D>
 static void launch_scores(const void* q, BinPlanes kb, float* scores, int32_t* pcs, int batch,
                           int hq, int hkv, int S, int stride, hipStream_t st) {
-    const int bx = (S + 255) / 256;
-    hipLaunchKernelGGL((scores_kernel<D>), dim3(bx < 1024 ? (bx < 1 ? 1 : bx) : 1024, batch * hq),
-                       dim3(256), 0, st, (const uint16_t*)q, kb, scores, pcs, hq, hkv, S, stride);
+    // about 8 workgroups per CU, each a chunk of at least 1024 keys
+    const int n_hb = (hq / hkv + kScoreHeads - 1) / kScoreHeads;
+    const int64_t rows = (int64_t)batch * hkv * n_hb;
+    const int64_t want = (8LL * bc::device_cu_count() + rows - 1) / rows;
+    const int64_t most = ((int64_t)S + 1023) / 1024;
+    const int n_chunks = (int)(want < most ? (want < 1 ? 1 : want) : most);
+    const int chunk = (S + n_chunks - 1) / n_chunks;
+    hipLaunchKernelGGL((scores_kernel<D>), dim3(n_chunks, (unsigned)rows), dim3(256), 0, st,
+                       (const uint16_t*)q, kb, scores, pcs, hq, hkv, S, stride, chunk, n_hb);
 }
 
 extern "C" int bc_binary_scores(const void* q, const void* k_bin, float* scores,

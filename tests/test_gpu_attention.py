@@ -96,11 +96,12 @@ def test_kv_stride_and_zero_length(F, H, Hkv, d):
     assert torch.count_nonzero(z) == 0
 
 
-@pytest.mark.parametrize("gqa", [1, 4])
-def test_binary_scores_exact(F, gqa):
-    say(f"case binary_scores gqa={gqa}")
-    B, Hq, S, d = 2, 8, 1500, 128
-    Hkv = Hq // gqa
+# (B, Hq, Hkv, S): MHA, GQA, and a group of 32 heads (two head batches per workgroup row)
+@pytest.mark.parametrize("shape", [(2, 8, 8, 1500), (2, 8, 2, 1500), (1, 32, 1, 700)])
+def test_binary_scores_exact(F, shape):
+    say(f"case binary_scores {shape}")
+    B, Hq, Hkv, S = shape
+    d = 128
     q, k, _ = make(B, Hq, Hkv, S, d, seed=11)
     kb = F.encode(torch.from_numpy(k.reshape(-1, d)).cuda())
     sc, pc = F.binary_scores(torch.from_numpy(q).cuda(), kb, B, Hq, S, d, n_kv_heads=Hkv)
