@@ -77,12 +77,14 @@ struct QDigits {
     float dq[G];                  // fixed-point step of q_int
 };
 
-// Per-wave LDS: two V staging buffers (tile i is consumed while tile i+1
-// lands), each the tile's code bytes then its sign bytes, then the (hi, lo)
-// fp16 weight columns [part][2G][64 slots].  The epilogue
-// reuses the region for [parts][G][D] partial sums (sign part, plus the
-// residual part when present) + G offsets.  Binary attention stages no codes.
-template <int D, int G, bool RES, int NSTAGE>
+// Per-wave LDS, one __shared__ array per role (the compiler tracks LDS
+// direct loads per array, so reading staging buffer i or the weights does not
+// wait for the direct loads still landing in buffer i+1): V staging buffers
+// (tile i is consumed while tile i+1 lands), each the tile's code bytes then
+// its sign bytes; the (hi, lo) fp16 weight columns [part][2G][64 slots]; the
+// K-side residual dots [64 keys][G] of GQA groups.  The epilogue reduces heads
+// in batches through staging buffer 0.  Binary attention stages no codes.
+template <int D, int G, bool RES>
 struct WaveLds {
     static constexpr int kCodeBytes = RES ? 64 * D / 2 : 0;
     // D = 64: 8-byte sign rows are copied two keys per lane by all 64 lanes
@@ -90,12 +92,10 @@ struct WaveLds {
     static constexpr int kSignBytes = 64 * D / 8 > 1024 ? 64 * D / 8 : 1024;
     static constexpr int kStage = kCodeBytes + kSignBytes;
     static constexpr int kWeightBytes = 2 * 2 * G * 64 * 2;
-    // K-side residual dots of all heads, [G][64 keys] int32 (GQA groups with
-    // the residual dot on the matrix cores)
-    static constexpr int kRdBytes = (G > 1 && RES) ? G * 64 * 4 : 0;
-    static constexpr int kMain = NSTAGE * kStage + kWeightBytes + kRdBytes;
-    static constexpr int kEpi = (((RES ? 2 : 1) * G * D + G) * 4 + 15) / 16 * 16;
-    static constexpr int kBytes = kMain > kEpi ? kMain : kEpi;
+    static constexpr int kRdInts = (G > 1 && RES) ? 64 * G : 4;
+    // epilogue: heads per pass through staging buffer 0 ([parts][heads][D] floats)
+    static constexpr int kEpiHeads = kStage / ((RES ? 2 : 1) * D * 4) < G ? kStage / ((RES ? 2 : 1) * D * 4) : G;
+    static_assert(kEpiHeads >= 1, "staging buffer holds one head's partial sums");
 };
 
 // K-side data of one 64-key tile held in registers: sign words and scales of
@@ -107,6 +107,12 @@ struct KRegs {
     uint16_t sk, svv, rsk, rsv;   // raw fp16 scales (converted at use, so the
                                   // loads of the next tile are not waited on)
 };
+
+// x through an empty asm: the compiler cannot split or re-associate it
+__device__ __forceinline__ int opaque_int(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
 
 __device__ __forceinline__ uint16_t f2h_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ __forceinline__ float h_bits2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -265,11 +271,15 @@ void attn_mfma_kernel(AttnArgs a) {
     // staging buffer and one K register set leave room for a third workgroup
     // per CU (measured faster); adaptive mode keeps it
     constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || (MODE == MODE_ADAPTIVE && BC_ADAPT_PIPE) || BC_GQA_PIPE;
-    using WL = WaveLds<D, G, RES, PIPE ? 2 : 1>;
+    using WL = WaveLds<D, G, RES>;
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
-    __shared__ __attribute__((aligned(16))) uint8_t wave_lds[4][WL::kBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_st0[4][WL::kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_st1[4][PIPE ? WL::kStage : 16];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][WL::kWeightBytes / 2];
+    __shared__ __attribute__((aligned(16))) int lds_rd[4][WL::kRdInts];
+    __shared__ float wofs[4][G];
     __shared__ float wm[4][G], wlsum[4][G], wsc[4];
 
     const int split = blockIdx.x;
@@ -294,14 +304,19 @@ void attn_mfma_kernel(AttnArgs a) {
     const int kown = LIN_K ? (lane % Q) * (64 / Q) + lane / Q : lane;
     const int quarter = lane % Q;
 
-    uint8_t* my = wave_lds[wave];
-    uint16_t* wts = (uint16_t*)(my + (PIPE ? 2 : 1) * WL::kStage);  // [2 parts][2G cols][64 slots]
-    int* rdl = (int*)((uint8_t*)wts + WL::kWeightBytes);  // [G][64] residual dots
-
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
     const int my_head = my_col >> 1;
     const int bcol = my_col < 2 * G ? my_col : (my_col & 1);
+
+    // weight columns [2 parts][2G cols][64 slots]: this lane's store slot in
+    // column 0, and its B-operand read position in column bcol.  The lane
+    // offsets go through an opaque copy so that every access is one constant
+    // offset from a base that the compiler ties to lds_wts (accesses it cannot
+    // tie to one array wait for all direct loads in flight, the prefetch too)
+    uint16_t* wsl = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + slot_of(kown));
+    const uint16_t* wrd = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + bcol * 64 + 16 * g4);
+    int* rdl = lds_rd[wave];          // [64 keys][G] residual dots
 
     // softmax reference per head, lowered lazily: weights p = 2^(s - m) stay
     // <= 2^kTau, and the accumulators are rescaled only when a score passes
@@ -424,7 +439,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // or piece c at c*1024 + 16k (per key)
     auto issue_v = [&](int buf, int t0) {
         const int tr = t0 - key_begin;
-        uint8_t* st_codes = my + buf * WL::kStage;
+        uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
         uint8_t* st_signs = st_codes + WL::kCodeBytes;
         if constexpr (SB >= 16) {
 #pragma unroll
@@ -448,7 +463,7 @@ void attn_mfma_kernel(AttnArgs a) {
 
     // ---------------- one tile: scores, online softmax, value MFMAs
     auto process = [&](const KRegs<D>& r, int t0, int buf) {
-        uint8_t* st_codes = my + buf * WL::kStage;
+        uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
         uint8_t* st_signs = st_codes + WL::kCodeBytes;
         const int s = t0 + kown;
         const bool valid = s < key_end;
@@ -658,7 +673,6 @@ void attn_mfma_kernel(AttnArgs a) {
         // online softmax; (hi, lo) fp16 weights to LDS in MFMA slot order
         float lane_alpha = 1.0f;
         bool any_rescale = false;
-        const int sl = slot_of(kown);
         // the value operands of odd keys come out 16x larger (see the MFMA
         // loops below): their weights carry 1/16 so that every product is exact
         const float kfac = (kown & 1) ? 0.0625f : 1.0f;
@@ -701,11 +715,11 @@ void attn_mfma_kernel(AttnArgs a) {
             // offset removed at the end, from the unrounded weights: the (hi, lo)
             // pairs carry ~22 bits, so the difference is a zero-mean ~2^-22 term
             off[g] = fmaf(p, fo, off[g]);
-            wts[(0 * 2 * G + 2 * g) * 64 + sl] = a2h;
-            wts[(0 * 2 * G + 2 * g + 1) * 64 + sl] = a2l;
+            wsl[(0 * 2 * G + 2 * g) * 64] = a2h;
+            wsl[(0 * 2 * G + 2 * g + 1) * 64] = a2l;
             if constexpr (RES) {
-                wts[(1 * 2 * G + 2 * g) * 64 + sl] = bh;
-                wts[(1 * 2 * G + 2 * g + 1) * 64 + sl] = bl;
+                wsl[(1 * 2 * G + 2 * g) * 64] = bh;
+                wsl[(1 * 2 * G + 2 * g + 1) * 64] = bl;
             }
         }
         if (any_rescale) {
@@ -736,8 +750,8 @@ void attn_mfma_kernel(AttnArgs a) {
         h8_t bsig[2], bres[2];
 #pragma unroll
         for (int mh = 0; mh < 2; mh++) {
-            bsig[mh] = *(const h8_t*)&wts[(0 * 2 * G + bcol) * 64 + 16 * g4 + 8 * mh];
-            if constexpr (RES) bres[mh] = *(const h8_t*)&wts[(1 * 2 * G + bcol) * 64 + 16 * g4 + 8 * mh];
+            bsig[mh] = *(const h8_t*)&wrd[(0 * 2 * G) * 64 + 8 * mh];
+            if constexpr (RES) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * 64 + 8 * mh];
             else bres[mh] = bsig[mh];
         }
 
@@ -814,7 +828,11 @@ void attn_mfma_kernel(AttnArgs a) {
     // ---------------- software-pipelined tile loop: tile i+1 loads in flight
     // while tile i computes (two register sets, two LDS staging buffers).  The
     // prefetch after a wave's last tile re-reads that tile (harmless, cached)
-    // so that no load sits behind a branch.
+    // so that no load sits behind a branch.  Every iteration of the two-tile
+    // loop starts with no load in flight: the compiler follows direct loads to
+    // LDS per staging buffer only within an iteration (across the back edge it
+    // would wait for all of them at the first staging-buffer read), so the
+    // prefetch issued before an iteration's second tile lands by its end.
     int t = key_begin + wave * 64;
     if (!PIPE) {
         for (; t < key_end; t += 4 * 64) {
@@ -829,10 +847,11 @@ void attn_mfma_kernel(AttnArgs a) {
         KRegs<D> ka, kb;
         load_k(ka, t);
         issue_v(0, t);
-        int tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
-        load_k(kb, tp);
-        issue_v(1, tp);
+        __builtin_amdgcn_s_waitcnt(0);
         for (;;) {
+            int tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+            load_k(kb, tp);
+            issue_v(1, tp);
             process(ka, t, 0);
             t += 4 * 64;
             if (t >= key_end) break;
@@ -842,17 +861,17 @@ void attn_mfma_kernel(AttnArgs a) {
             process(kb, t, 1);
             t += 4 * 64;
             if (t >= key_end) break;
-            tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
-            load_k(kb, tp);
-            issue_v(1, tp);
+            __builtin_amdgcn_s_waitcnt(0);
         }
         // the last prefetch still writes LDS that the epilogue reuses
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
     }
 
-    // ---------------- epilogue: per wave, per head: acc[e] = ((cs + cn) * 2^24 - off) * 2^-wexp
-    float* accw = (float*)my;  // [2 parts][G][D] floats + G offsets
+    // ---------------- epilogue: per wave, per head: acc[e] = ((cs + cn) * 2^24 - off) * 2^-wexp,
+    // then the four waves' partials are merged.  Heads pass through staging
+    // buffer 0 kEpiHeads at a time ([parts][kEpiHeads][D] floats per wave).
+    constexpr int HP = WL::kEpiHeads;
     const float two24 = 16777216.0f;
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -861,59 +880,61 @@ void attn_mfma_kernel(AttnArgs a) {
         if (lane == 0) {
             wm[wave][g] = m[g];
             wlsum[wave][g] = l_w;
-            wsc[wave] = ldexpf(1.0f, -wexp);
-            accw[(RES ? 2 : 1) * G * D + g] = o_w;  // stash after the arrays
+            wofs[wave][g] = o_w;
         }
     }
-    // hi + lo columns are adjacent lanes (col 2g, 2g+1)
+    if (lane == 0) wsc[wave] = ldexpf(1.0f, -wexp);
+    float* accw = (float*)lds_st0[wave];
+    // hi + lo columns are adjacent lanes (col 2g, 2g+1); the even lane writes
+    const bool writer = my_col < 2 * G && (my_col & 1) == 0;
+    for (int g0 = 0; g0 < G; g0 += HP) {
+        const int hs = my_head - g0;   // this lane's head slot in the batch
+        const bool wr = writer && hs >= 0 && hs < HP;
+        if (g0 > 0) __syncthreads();   // the previous batch has been read
 #pragma unroll
-    for (int h = 0; h < NH; h++)
+        for (int h = 0; h < NH; h++)
 #pragma unroll
-        for (int p = 0; p < 4; p++)
+            for (int p = 0; p < 4; p++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                // accumulator p carries 2^p (bit p read in place)
-                const float v = (cs[h][p][i] + __shfl_xor(cs[h][p][i], 1, 64)) * (1.0f / (float)(1 << p));
-                if (my_col < 2 * G && (my_col & 1) == 0) {
-                    const int dim = 64 * h + 4 * (4 * g4 + i) + p;
-                    accw[(0 * G + my_head) * D + dim] = v;
+                for (int i = 0; i < 4; i++) {
+                    // accumulator p carries 2^p (bit p read in place)
+                    const float v = (cs[h][p][i] + __shfl_xor(cs[h][p][i], 1, 64)) * (1.0f / (float)(1 << p));
+                    if (wr) accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = v;
                 }
-            }
-    if constexpr (RES) {
+        if constexpr (RES) {
 #pragma unroll
-        for (int d = 0; d < NB; d++)
+            for (int d = 0; d < NB; d++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float v = cn[d][i] + __shfl_xor(cn[d][i], 1, 64);
-                if (my_col < 2 * G && (my_col & 1) == 0) {
-                    const int dim = 16 * d + 4 * g4 + i;
-                    accw[(1 * G + my_head) * D + dim] = v;
+                for (int i = 0; i < 4; i++) {
+                    const float v = cn[d][i] + __shfl_xor(cn[d][i], 1, 64);
+                    if (wr) accw[(1 * HP + hs) * D + 16 * d + 4 * g4 + i] = v;
                 }
-            }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
-        const int g = i / D, e = i % D;
-        float M = -INFINITY;
-        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
-        float accv = 0.0f, lv = 0.0f;
-        if (M != -INFINITY) {
-            for (int w = 0; w < 4; w++) {
-                if (wm[w][g] == -INFINITY) continue;
-                const float f = exp2f(wm[w][g] - M);
-                const float* aw = (const float*)wave_lds[w];
-                float v = aw[(0 * G + g) * D + e];
-                if (RES) v += aw[(1 * G + g) * D + e];
-                v = (v * two24 - aw[(RES ? 2 : 1) * G * D + g]) * wsc[w];
-                accv += f * v;
-                lv += f * wlsum[w][g];
-            }
         }
-        float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
-        dst[2 + e] = accv;
-        if (e == 0) {
-            dst[0] = M;
-            dst[1] = lv;
+        __syncthreads();
+        const int nh = min(HP, G - g0);
+        for (int i = threadIdx.x; i < nh * D; i += blockDim.x) {
+            const int hs2 = i / D, e = i % D, g = g0 + hs2;
+            float M = -INFINITY;
+            for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+            float accv = 0.0f, lv = 0.0f;
+            if (M != -INFINITY) {
+                for (int w = 0; w < 4; w++) {
+                    if (wm[w][g] == -INFINITY) continue;
+                    const float f = exp2f(wm[w][g] - M);
+                    const float* aw = (const float*)lds_st0[w];
+                    float v = aw[(0 * HP + hs2) * D + e];
+                    if (RES) v += aw[(1 * HP + hs2) * D + e];
+                    v = (v * two24 - wofs[w][g]) * wsc[w];
+                    accv += f * v;
+                    lv += f * wlsum[w][g];
+                }
+            }
+            float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
+            dst[2 + e] = accv;
+            if (e == 0) {
+                dst[0] = M;
+                dst[1] = lv;
+            }
         }
     }
 }
