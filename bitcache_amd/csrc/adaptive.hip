@@ -13,21 +13,28 @@
 // (b, head) then scans only that chunk for the cutoff index.  The attention
 // kernel selects key > T, or key == T at an index <= cutoff.
 //
+// The first pass computes the popcounts from the K sign planes and stores
+// them (one byte per query head and key; two for d = 256), so the later
+// passes, the tie scan and the attention pass read those instead of the
+// d/8-byte sign rows.
+//
 // Workspace: hist [B*Hq][2048] u32 | prefix [B*Hq] u32 | remain [B*Hq] i32
 //            | cutoff [B*Hq] i32 | chunk histograms [B*Hq][nsplit][1024] u32
-//            | attention partials.
-#include "common.h"
+//            | popcounts [B*Hq/G][S][G] | attention partials.
+#include "attn.h"
 
 namespace bc {
 int run_attention(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* cutoff, uint8_t* selected);
+                  const int32_t* cutoff, uint8_t* selected, const void* pcs);
 size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
 }  // namespace bc
 
 namespace {
+using bc::PcPack;
+using bc::PcT;
 
 constexpr int kBins = 2048;
 
@@ -41,6 +48,7 @@ struct SelArgs {
     int32_t* remain;     // [B*Hq]
     int32_t* cutoff;     // [B*Hq]
     uint32_t* chist;     // [B*Hq][nsplit][1024] last-pass histogram of each chunk
+    void* pcs;           // [B*Hq/G][S][G] popcounts (PcT<D>)
 };
 
 template <int D, int G>
@@ -54,10 +62,15 @@ __device__ void load_q_signs(const uint16_t* qb, uint32_t (*qs)[D / 32]) {
 }
 
 template <int D>
-__device__ __forceinline__ uint32_t key_of(const uint32_t* qs, const SignWords<D>& ks, float sk) {
+__device__ __forceinline__ int popc_of(const uint32_t* qs, const SignWords<D>& ks) {
     int pc = 0;
 #pragma unroll
     for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
+    return pc;
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t key_of_pc(int pc, float sk) {
     return ordered_key(sk * (float)(2 * pc - D));
 }
 
@@ -82,24 +95,46 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
     for (int g = 0; g < G; g++) pref[g] = pass == 0 ? 0u : a.prefix[bhq0 + g];
     const int64_t base = (int64_t)bkv * a.kv_stride;
     const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
+    using P = PcT<D>;
+    using Pack = PcPack<P, G>;
+    Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * a.S;   // this group's [S] packs
     // four keys per thread per iteration, all loads issued first
     constexpr int U = 4;
     for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
-        SignWords<D> ks[U];
+        Pack pk[U];
         float sk[U];
+        if (pass == 0) {
+            // popcounts from the sign rows, stored for the later passes
+            SignWords<D> ks[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int ss = s + u * blockDim.x;
-            const int64_t i = base + (ss < k1 ? ss : s);
-            ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
-            sk[u] = h2f(a.kb.scales[i]);
+            for (int u = 0; u < U; u++) {
+                const int ss = s + u * blockDim.x;
+                const int64_t i = base + (ss < k1 ? ss : s);
+                ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
+                sk[u] = h2f(a.kb.scales[i]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+#pragma unroll
+                for (int g = 0; g < G; g++) pk[u].v[g] = (P)popc_of<D>(qs[g], ks[u]);
+                const int ss = s + u * blockDim.x;
+                if (ss < k1) pcs[ss] = pk[u];
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int ss = s + u * blockDim.x;
+                const int sc = ss < k1 ? ss : s;
+                pk[u] = pcs[sc];
+                sk[u] = h2f(a.kb.scales[base + sc]);
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (s + u * (int)blockDim.x >= k1) break;
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const uint32_t key = key_of<D>(qs[g], ks[u], sk[u]);
+                const uint32_t key = key_of_pc<D>((int)pk[u].v[g], sk[u]);
                 const bool match = pbits == 0 || (key >> (32 - pbits)) == (pref[g] >> (32 - pbits));
                 if (match) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
             }
@@ -181,23 +216,25 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_
 }
 
 // Cutoff index of the ties at the final threshold T: one block per (b, query
-// head).  The chunk histograms give the chunk holding the need-th tie; that
-// chunk is scanned in key order, 256 keys at a time.
-template <int D>
+// head).  The chunk histograms give the chunk holding the need-th tie; in that
+// chunk each thread counts the ties of a contiguous run of keys (stored
+// popcounts and K scales), a block prefix sum finds the run holding the
+// rank-th tie, and that thread walks its run for the key index.
+template <int D, int G>
 __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
-    __shared__ uint32_t qs[1][D / 32];
     __shared__ int sh_chunk, sh_rank;
-    __shared__ int wcount[4][4];
+    __shared__ uint32_t part[256];
+    using Pack = PcPack<PcT<D>, G>;
     const int bhq = blockIdx.x;
     const int b = bhq / a.Hq, h = bhq % a.Hq;
     const int kvh = h / (a.Hq / a.Hkv);
+    const int g = bhq % G;   // head slot in its group (groups are G consecutive heads)
     const int need = a.remain[bhq];
     if (need <= 0) {
         if (threadIdx.x == 0) a.cutoff[bhq] = -1;
         return;
     }
     const uint32_t T = a.prefix[bhq];
-    load_q_signs<D, 1>(a.q + (int64_t)bhq * D, qs);
     if (threadIdx.x == 0) {
         const uint32_t* ch = a.chist + (int64_t)bhq * a.nsplit * 1024 + (T & 0x3FFu);
         int cum = 0, c = 0;
@@ -211,55 +248,46 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     }
     __syncthreads();
     const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
+    const Pack* pcs = (const Pack*)a.pcs + (int64_t)(bhq - g) / G * a.S;
     const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint64_t below = (1ull << lane) - 1ull;
-    int rank = sh_rank;
-    int found = -1;
-    // 1024 keys per step (4 per thread, loads first); key order = u, wave, lane
-    for (int s0 = k0; s0 < k1; s0 += 1024) {
-        bool tie[4];
-        SignWords<D> ks[4];
-        float sk[4];
+    const int per = (a.chunk + 255) / 256;
+    const int s0 = min(k1, k0 + (int)threadIdx.x * per), s1 = min(k1, s0 + per);
+    auto is_tie = [&](int s) {
+        return key_of_pc<D>((int)pcs[s].v[g], h2f(a.kb.scales[base + s])) == T;
+    };
+    uint32_t cnt = 0;
+    int s = s0;
+    for (; s + 8 <= s1; s += 8) {
+        bool t8[8];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int s = s0 + u * 256 + (int)threadIdx.x;
-            const int64_t i = base + (s < k1 ? s : k0);
-            ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
-            sk[u] = h2f(a.kb.scales[i]);
-        }
-        uint64_t m[4];
+        for (int u = 0; u < 8; u++) t8[u] = is_tie(s + u);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int s = s0 + u * 256 + (int)threadIdx.x;
-            tie[u] = s < k1 && key_of<D>(qs[0], ks[u], sk[u]) == T;
-            m[u] = __ballot(tie[u]);
-            if (lane == 0) wcount[u][wave] = __builtin_popcountll(m[u]);
-        }
+        for (int u = 0; u < 8; u++) cnt += t8[u] ? 1u : 0u;
+    }
+    for (; s < s1; s++) cnt += is_tie(s) ? 1u : 0u;
+    // inclusive prefix over the 256 runs (Hillis-Steele in LDS)
+    part[threadIdx.x] = cnt;
+    __syncthreads();
+    uint32_t incl = cnt;
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
         __syncthreads();
-        bool done = false;
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            int before = 0, total = 0;
-            for (int w = 0; w < 4; w++) {
-                if (w < wave) before += wcount[u][w];
-                total += wcount[u][w];
-            }
-            if (!done) {
-                if (rank <= total) {
-                    const int mine = before + __builtin_popcountll(m[u] & below) + 1;
-                    if (tie[u] && mine == rank) found = s0 + u * 256 + (int)threadIdx.x;
-                    done = true;
-                } else {
-                    rank -= total;
-                }
-            }
-        }
-        if (done) break;
+        incl += add;
+        part[threadIdx.x] = incl;
         __syncthreads();
     }
-    // exactly one thread found it (rank <= ties in the chunk by construction)
-    if (found >= 0) a.cutoff[bhq] = found;
+    const uint32_t excl = incl - cnt;
+    const uint32_t rank = (uint32_t)sh_rank;
+    // exactly one run holds it (rank <= ties in the chunk by construction)
+    if (excl < rank && incl >= rank) {
+        uint32_t r = rank - excl;
+        for (int k = s0; k < s1; k++) {
+            if (is_tie(k) && --r == 0) {
+                a.cutoff[bhq] = k;
+                break;
+            }
+        }
+    }
 }
 
 __global__ void zero_kernel(uint32_t* p, int64_t n) {
@@ -295,7 +323,7 @@ Chunks chunks_for(int batch, int hq, int hkv, int S) {
 }
 
 struct Layout {
-    size_t hist, prefix, remain, cutoff, chist, attn, total;
+    size_t hist, prefix, remain, cutoff, chist, pcs, attn, total;
 };
 
 Layout layout(int batch, int hq, int hkv, int S, int d) {
@@ -308,7 +336,8 @@ Layout layout(int batch, int hq, int hkv, int S, int d) {
     L.remain = al(L.prefix + bh * 4);
     L.cutoff = al(L.remain + bh * 4);
     L.chist = al(L.cutoff + bh * 4);
-    L.attn = al(L.chist + bh * (size_t)c.nsplit * 1024 * 4);
+    L.pcs = al(L.chist + bh * (size_t)c.nsplit * 1024 * 4);
+    L.attn = al(L.pcs + bh * (size_t)S * (d > 255 ? 2 : 1));
     L.total = L.attn + bc::attention_ws_bytes(batch, hq, hkv, S, d);
     return L;
 }
@@ -321,7 +350,7 @@ void run_passes(const SelArgs& a, int splits_y, int chunk, int nsplit, int bh, i
         hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a, pass, chunk);
         hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, pass, top_k);
     }
-    hipLaunchKernelGGL((tie_locate_kernel<D>), dim3(bh), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((tie_locate_kernel<D, G>), dim3(bh), dim3(256), 0, st, a);
 }
 
 template <int D>
@@ -380,6 +409,7 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     a.remain = (int32_t*)(ws + L.remain);
     a.cutoff = (int32_t*)(ws + L.cutoff);
     a.chist = (uint32_t*)(ws + L.chist);
+    a.pcs = ws + L.pcs;
     // clear the histograms with a kernel (no memset nodes: graph-capture safe)
     hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, a.hist, (int64_t)bh * kBins);
     int rc = bc::check_launch("adaptive zero");
@@ -406,5 +436,5 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     if (rc != BC_OK) return rc;
     return bc::run_attention(2, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
                              seq_len, kv_stride, head_dim, ws + L.attn, workspace_bytes - L.attn,
-                             st, a.prefix, a.cutoff, selected);
+                             st, a.prefix, a.cutoff, selected, a.pcs);
 }

@@ -834,7 +834,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
                 const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
                 hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
-                uint8_t* selected) {
+                uint8_t* selected, const void* pcs) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -863,6 +863,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.thresh = thresh;
     a.cutoff = cutoff;
     a.selected = selected;
+    a.pcs = pcs;
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     // matrix-core value phase for head_dim 64/128/256; the VALU kernel covers the
     // other head dims (and is selectable with BITCACHE_VALU_ATTENTION=1)
@@ -892,10 +893,10 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* cutoff, uint8_t* selected) {
+                  const int32_t* cutoff, uint8_t* selected, const void* pcs) {
     int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
                          kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
-                         selected);
+                         selected, pcs);
     if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
@@ -925,7 +926,7 @@ extern "C" int bc_attention_partial(const void* q, const void* k_bin, const void
                "k_res and v_res must both be given or both be null");
     return bc::run_partial(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, batch,
                            n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
-                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads,
@@ -939,7 +940,7 @@ extern "C" int bc_binary_attention(const void* q, const void* k_bin, const void*
                                    void* workspace, size_t workspace_bytes, void* stream) {
     return bc::run_attention(MODE_BINARY, q, k_bin, nullptr, v_bin, nullptr, out, batch, n_heads,
                              n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
-                             (hipStream_t)stream, nullptr, nullptr, nullptr);
+                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_compensated_attention(const void* q, const void* k_bin, const void* k_res,
@@ -948,7 +949,7 @@ extern "C" int bc_compensated_attention(const void* q, const void* k_bin, const 
                                         size_t workspace_bytes, void* stream) {
     return bc::run_attention(MODE_COMP, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads,
                              n_heads, seq_len, seq_len, head_dim, workspace, workspace_bytes,
-                             (hipStream_t)stream, nullptr, nullptr, nullptr);
+                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
 }
 
 extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_res,
@@ -960,7 +961,7 @@ extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_
                "k_res and v_res must both be given or both be null");
     return bc::run_attention(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, out,
                              batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
-                             workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                             workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
 }
 
 template <int D>

@@ -102,10 +102,12 @@ struct WaveLds {
 // the lane's own key, and the lane's code pieces (see the kernel).
 template <int D>
 struct KRegs {
-    SignWords<D> ks;
-    uint32_t kc[D / 8];
+    SignWords<D> ks;              // (adaptive mode: the stored popcounts instead)
+    uint32_t pcw[4];              // adaptive: the G popcounts of the lane's key
+    uint32_t kc[D / 8];           // (adaptive mode: gathered later, selected keys)
     uint16_t sk, svv, rsk, rsv;   // raw fp16 scales (converted at use, so the
                                   // loads of the next tile are not waited on)
+    uint32_t sel;                 // adaptive: bit g = head g selected the lane's key
 };
 
 // x through an empty asm: the compiler cannot split or re-associate it
@@ -218,12 +220,16 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_BIN_WAVES
 #define BC_BIN_WAVES 5
 #endif
+#ifndef BC_ADAPT_WAVES
+#define BC_ADAPT_WAVES 2
+#endif
 template <int D, int G, int MODE>
 struct Occupancy {
     static constexpr int kWaves =
-        MODE == MODE_BINARY ? (D <= 128 ? (G <= 2 ? BC_BIN_WAVES : 3) : 2)
-                            : ((G == 1 && D <= 128) ? BC_MHA_WAVES
-                                                    : (D <= 128 ? (G <= 4 && !BC_GQA_PIPE && (MODE == MODE_COMP || !BC_ADAPT_PIPE) ? 3 : 2) : 1));
+        MODE == MODE_BINARY     ? (D <= 128 ? (G <= 2 ? BC_BIN_WAVES : 3) : 2)
+        : MODE == MODE_ADAPTIVE ? (D <= 128 ? BC_ADAPT_WAVES : 1)
+        : (G == 1 && D <= 128)  ? BC_MHA_WAVES
+                                : (D <= 128 ? (G <= 4 && !BC_GQA_PIPE ? 3 : 2) : 1);
 };
 
 // Sum of v over the Q consecutive lanes that share one key row (DPP, no LDS).
@@ -397,11 +403,42 @@ void attn_mfma_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t r_ksc = rsrc(a.kb.scales, 2), r_vsc = rsrc(a.vb.scales, 2);
     const __amdgpu_buffer_rsrc_t r_kc = rsrc(a.kr.codes, CB), r_vc = rsrc(a.vr.codes, CB);
     const __amdgpu_buffer_rsrc_t r_krs = rsrc(a.kr.scales, 2), r_vrs = rsrc(a.vr.scales, 2);
+    // adaptive: stored popcounts of this group, one pack of G per key
+    using Pack = bc::PcPack<bc::PcT<D>, G>;
+    constexpr int kPack = (int)sizeof(Pack);
+    static_assert(kPack <= 16, "one load per pack");
+    const __amdgpu_buffer_rsrc_t r_pc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const Pack*)a.pcs + (int64_t)bhq0 / G * a.S + key_begin), (short)0, nk * kPack, kBufWord3);
+    // an offset past every range (the host keeps each range's bytes below
+    // 2^31 - 4096): such a load returns zeros and moves no data
+    constexpr int kOob = 0x7FFFF000;
 
     // ---------------- loads of one tile: K side into registers, V side to LDS
     auto load_k = [&](KRegs<D>& r, int t0) {
         const int tr = t0 - key_begin;      // tile offset in the range (keys)
         const int kk = tr + kown;
+        if constexpr (MODE == MODE_ADAPTIVE) {
+            // popcounts and the two binary scales; residual data is gathered
+            // once the tile's selection is known
+            if constexpr (kPack == 1) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b8(r_pc, kk, 0, 0);
+            } else if constexpr (kPack == 2) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b16(r_pc, kk * 2, 0, 0);
+            } else if constexpr (kPack == 4) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b32(r_pc, kk * 4, 0, 0);
+            } else if constexpr (kPack == 8) {
+                const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r_pc, kk * 8, 0, 0);
+                r.pcw[0] = v[0]; r.pcw[1] = v[1];
+            } else {
+                const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pc, kk * 16, 0, 0);
+                r.pcw[0] = v[0]; r.pcw[1] = v[1]; r.pcw[2] = v[2]; r.pcw[3] = v[3];
+            }
+            r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
+            r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
+            r.rsk = 0;
+            r.rsv = 0;
+            return;
+        }
         r.ks = buf_signs<D>(r_ks, kk * SB);
         r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
         r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
@@ -461,6 +498,62 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     };
 
+    // ---------------- adaptive mode: a tile's selection, from its stored
+    // popcounts and K scales, and the loads of its residual data (K codes and
+    // residual scales to registers, V codes with the V signs to staging buffer
+    // buf).  The lanes of keys no head selected load from past the range
+    // (zeros, no traffic), so the loads issue without branches.
+    auto gather = [&](KRegs<D>& r, int t0, int buf) {
+        const int s = t0 + kown;
+        const bool valid = s < key_end;
+        const float sk = h2f(r.sk);
+        uint32_t selmask = 0;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            constexpr int bits = 8 * (int)sizeof(bc::PcT<D>);
+            constexpr int per_word = 32 / bits;
+            const int pc = (int)((r.pcw[g / per_word] >> (bits * (g % per_word))) & ((1u << bits) - 1u));
+            // selected: above the threshold, or equal to it at an index up to
+            // the cutoff (ties are taken lowest index first)
+            const uint32_t key = ordered_key(sk * (float)(2 * pc - D));
+            const bool sel = key > thresh[g] || (key == thresh[g] && s <= cutoff[g]);
+            selmask |= (sel && valid) ? (1u << g) : 0u;
+        }
+        r.sel = selmask;
+        issue_v(buf, t0);
+        uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
+        const uint64_t selany = __ballot(selmask != 0u);
+        const int tr = t0 - key_begin;
+        const bool mine = selmask != 0u;
+        const int kk = tr + kown;
+        r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, mine ? kk * 2 : kOob, 0, 0);
+        r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, mine ? kk * 2 : kOob, 0, 0);
+        if constexpr (KMF) {
+            // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const bool sel_k = (selany >> (16 * kb + lj)) & 1ull;
+                const int base = sel_k ? (tr + 16 * kb + lj) * CB + 16 * g4 : kOob;
+#pragma unroll
+                for (int pc = 0; pc < NPC; pc++) {
+                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 64 * pc, 0, 0);
+                    const int i = kb * NPC + pc;
+                    r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, mine ? kk * CB + 16 * i : kOob, 0, 0);
+                r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < Q; c++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
+                                                     mine ? kk * CB + 16 * c : kOob, 0, 0, 0);
+    };
+
     // ---------------- one tile: scores, online softmax, value MFMAs
     auto process = [&](const KRegs<D>& r, int t0, int buf) {
         uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
@@ -490,25 +583,20 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             int pc = 0;
+            if constexpr (MODE == MODE_ADAPTIVE) {
+                // stored by the selection passes (same popcount as below)
+                constexpr int bits = 8 * (int)sizeof(bc::PcT<D>);
+                constexpr int per_word = 32 / bits;
+                pc = (int)((r.pcw[g / per_word] >> (bits * (g % per_word))) & ((1u << bits) - 1u));
+            } else {
 #pragma unroll
-            for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qd.signs[g][w] ^ r.ks.w[w]));
+                for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qd.signs[g][w] ^ r.ks.w[w]));
+            }
             const float mq = (float)(2 * pc - D);
             xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:179)
-            if constexpr (MODE == MODE_ADAPTIVE) {
-                // selected: above the threshold, or equal to it at an index up to
-                // the cutoff (ties are taken lowest index first)
-                const uint32_t key = ordered_key(sk * mq);
-                const bool sel = key > thresh[g] || (key == thresh[g] && s <= cutoff[g]);
-                selmask |= (sel && valid) ? (1u << g) : 0u;
-            }
         }
+        if constexpr (MODE == MODE_ADAPTIVE) selmask = r.sel;
         if constexpr (MODE == MODE_ADAPTIVE) {
-            if (selmask) {
-#pragma unroll
-                for (int c = 0; c < Q; c++)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
-                                                             (s - key_begin) * CB + 16 * c, 0, 0, 0);
-            }
             if (a.selected != nullptr && valid) {
 #pragma unroll
                 for (int g = 0; g < G; g++)
@@ -738,9 +826,10 @@ void attn_mfma_kernel(AttnArgs a) {
         if constexpr (MODE != MODE_ADAPTIVE && PIPE) {
             constexpr int n = kPrefetchOps;
             __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-        } else {
+        } else if constexpr (MODE != MODE_ADAPTIVE) {
             __builtin_amdgcn_s_waitcnt(0);
         }
+        // (adaptive mode: the compiler waits for this staging buffer's loads)
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the weight stores above
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -834,7 +923,41 @@ void attn_mfma_kernel(AttnArgs a) {
     // would wait for all of them at the first staging-buffer read), so the
     // prefetch issued before an iteration's second tile lands by its end.
     int t = key_begin + wave * 64;
-    if (!PIPE) {
+    if constexpr (MODE == MODE_ADAPTIVE) {
+        // popcounts and binary scales two tiles ahead, selection and residual
+        // gathers one tile ahead; each iteration (two tiles) starts with no
+        // load in flight and every load has a tile of compute to land
+        if (t < key_end) {
+            KRegs<D> ra, rb, rc, rd;
+            load_k(ra, t);
+            load_k(rb, t + 4 * 64);
+            gather(ra, t, 0);
+            __builtin_amdgcn_s_waitcnt(0);
+            for (;;) {
+                const int t1 = t + 4 * 64;
+                gather(rb, t1, 1);
+                load_k(rc, t + 8 * 64);
+                load_k(rd, t + 12 * 64);
+                process(ra, t, 0);
+                if (t1 >= key_end) break;
+                // ra is free: it takes the popcounts and scales of tile t + 512
+                // and receives that tile's residual gathers
+                ra.pcw[0] = rc.pcw[0]; ra.pcw[1] = rc.pcw[1]; ra.pcw[2] = rc.pcw[2]; ra.pcw[3] = rc.pcw[3];
+                ra.sk = rc.sk;
+                ra.svv = rc.svv;
+                gather(ra, t + 8 * 64, 0);
+                process(rb, t1, 1);
+                t += 8 * 64;
+                if (t >= key_end) break;
+                __builtin_amdgcn_s_waitcnt(0);
+                rb.pcw[0] = rd.pcw[0]; rb.pcw[1] = rd.pcw[1]; rb.pcw[2] = rd.pcw[2]; rb.pcw[3] = rd.pcw[3];
+                rb.sk = rd.sk;
+                rb.svv = rd.svv;
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_wave_barrier();
+        }
+    } else if (!PIPE) {
         for (; t < key_end; t += 4 * 64) {
             KRegs<D> ka;
             load_k(ka, t);
@@ -966,6 +1089,8 @@ namespace bc {
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
     // buffer offsets inside one split's key range are 32-bit
     if ((int64_t)a.chunk * (D / 2) + 4096 >= ((int64_t)1 << 31)) return false;
+    // adaptive mode reads the popcounts stored by the selection passes
+    if (mode == MODE_ADAPTIVE && a.pcs == nullptr) return false;
     switch (D) {
         case 64: launch_d<64>(mode, G, a, grid, st); return true;
         case 128: launch_d<128>(mode, G, a, grid, st); return true;

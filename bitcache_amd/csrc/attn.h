@@ -22,6 +22,18 @@ struct AttnArgs {
     const int32_t* cutoff;       // [B*Hq] keys equal to the threshold are taken up to
                                  // this key index (-1: none)
     uint8_t* selected;           // optional [B, Hq, S]
+    const void* pcs;             // adaptive: [B*Hq/G][S] PcPack<PcT<D>, G> popcounts of
+                                 // the selection passes (G = the kernel's head group)
+};
+
+// Stored popcount of one (query head, key): 8 bits, 16 for d = 256 (popcount
+// up to 256).  A pack holds the G heads of a query-head group for one key.
+template <bool WIDE> struct PcSel { typedef uint8_t type; };
+template <> struct PcSel<true> { typedef uint16_t type; };
+template <int D> using PcT = typename PcSel<(D > 255)>::type;
+template <typename P, int G>
+struct __attribute__((aligned(G * sizeof(P)))) PcPack {
+    P v[G];
 };
 
 // MFMA value-phase kernels (attention_mfma.hip): true if (D, G, mode) is
