@@ -216,14 +216,12 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_
 }
 
 // Cutoff index of the ties at the final threshold T: one block per (b, query
-// head).  The chunk histograms give the chunk holding the need-th tie; in that
-// chunk each thread counts the ties of a contiguous run of keys (stored
-// popcounts and K scales), a block prefix sum finds the run holding the
-// rank-th tie, and that thread walks its run for the key index.
+// head).  The chunk histograms give the chunk holding the need-th tie; that
+// chunk is scanned from the stored popcounts and K scales (see below).
 template <int D, int G>
 __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
-    __shared__ int sh_chunk, sh_rank;
-    __shared__ uint32_t part[256];
+    __shared__ int sh_chunk, sh_rank, sh_total;
+    __shared__ uint64_t tmask[64][4];   // [stripe][wave] tie ballots of a window
     using Pack = PcPack<PcT<D>, G>;
     const int bhq = blockIdx.x;
     const int b = bhq / a.Hq, h = bhq % a.Hq;
@@ -250,43 +248,63 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
     const Pack* pcs = (const Pack*)a.pcs + (int64_t)(bhq - g) / G * a.S;
     const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
-    const int per = (a.chunk + 255) / 256;
-    const int s0 = min(k1, k0 + (int)threadIdx.x * per), s1 = min(k1, s0 + per);
-    auto is_tie = [&](int s) {
-        return key_of_pc<D>((int)pcs[s].v[g], h2f(a.kb.scales[base + s])) == T;
-    };
-    uint32_t cnt = 0;
-    int s = s0;
-    for (; s + 8 <= s1; s += 8) {
-        bool t8[8];
+    // windows of 64 stripes of 256 keys, read coalesced (all loads of 16
+    // stripes issued first); a wave ballot per stripe records the ties; one
+    // wave prefix-sums the 64 stripe counts, finds the stripe holding the
+    // rank-th tie, and picks the key from that stripe's per-wave masks
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int rank = sh_rank;
+    for (int w0 = k0; w0 < k1; w0 += 256 * 64) {
+        for (int b0 = 0; b0 < 64; b0 += 16) {
+            int pcv[16];
+            float skv[16];
 #pragma unroll
-        for (int u = 0; u < 8; u++) t8[u] = is_tie(s + u);
+            for (int u = 0; u < 16; u++) {
+                const int sv = w0 + (b0 + u) * 256 + (int)threadIdx.x;
+                const int sc = sv < k1 ? sv : k0;
+                pcv[u] = (int)pcs[sc].v[g];
+                skv[u] = h2f(a.kb.scales[base + sc]);
+            }
 #pragma unroll
-        for (int u = 0; u < 8; u++) cnt += t8[u] ? 1u : 0u;
-    }
-    for (; s < s1; s++) cnt += is_tie(s) ? 1u : 0u;
-    // inclusive prefix over the 256 runs (Hillis-Steele in LDS)
-    part[threadIdx.x] = cnt;
-    __syncthreads();
-    uint32_t incl = cnt;
-    for (int off = 1; off < 256; off <<= 1) {
-        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
-        __syncthreads();
-        incl += add;
-        part[threadIdx.x] = incl;
-        __syncthreads();
-    }
-    const uint32_t excl = incl - cnt;
-    const uint32_t rank = (uint32_t)sh_rank;
-    // exactly one run holds it (rank <= ties in the chunk by construction)
-    if (excl < rank && incl >= rank) {
-        uint32_t r = rank - excl;
-        for (int k = s0; k < s1; k++) {
-            if (is_tie(k) && --r == 0) {
-                a.cutoff[bhq] = k;
-                break;
+            for (int u = 0; u < 16; u++) {
+                const int sv = w0 + (b0 + u) * 256 + (int)threadIdx.x;
+                const uint64_t m = __ballot(sv < k1 && key_of_pc<D>(pcv[u], skv[u]) == T);
+                if (lane == 0) tmask[b0 + u][wave] = m;
             }
         }
+        __syncthreads();
+        if (wave == 0) {
+            const int j = lane;   // stripe
+            const uint32_t c = (uint32_t)(__builtin_popcountll(tmask[j][0]) + __builtin_popcountll(tmask[j][1]) +
+                                          __builtin_popcountll(tmask[j][2]) + __builtin_popcountll(tmask[j][3]));
+            uint32_t incl = c;
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t up = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += up;
+            }
+            const uint32_t excl = incl - c;
+            if (excl < (uint32_t)rank && incl >= (uint32_t)rank) {
+                uint32_t r = (uint32_t)rank - excl;
+                for (int w = 0; w < 4; w++) {
+                    const uint64_t m = tmask[j][w];
+                    const uint32_t cw = (uint32_t)__builtin_popcountll(m);
+                    if (r <= cw) {
+                        for (int i = 0; i < 64; i++) {
+                            if (((m >> i) & 1ull) && --r == 0) {
+                                a.cutoff[bhq] = w0 + j * 256 + w * 64 + i;
+                                break;
+                            }
+                        }
+                        break;
+                    }
+                    r -= cw;
+                }
+            }
+            if (lane == 63) sh_total = (int)incl;
+        }
+        __syncthreads();
+        if (sh_total >= rank) break;   // found in this window
+        rank -= sh_total;
     }
 }
 
