@@ -98,14 +98,21 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
     using P = PcT<D>;
     using Pack = PcPack<P, G>;
     Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * a.S;   // this group's [S] packs
-    // four keys per thread per iteration, all loads issued first
-    constexpr int U = 4;
-    for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
-        Pack pk[U];
-        float sk[U];
-        if (pass == 0) {
-            // popcounts from the sign rows, stored for the later passes
+    auto count = [&](const Pack& pk, float sk) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint32_t key = key_of_pc<D>((int)pk.v[g], sk);
+            const bool match = pbits == 0 || (key >> (32 - pbits)) == (pref[g] >> (32 - pbits));
+            if (match) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+        }
+    };
+    if (pass == 0) {
+        // popcounts from the sign rows, stored for the later passes; eight
+        // keys per thread per iteration, all loads issued first
+        constexpr int U = 8;
+        for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
             SignWords<D> ks[U];
+            float sk[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int ss = s + u * blockDim.x;
@@ -115,12 +122,21 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
-#pragma unroll
-                for (int g = 0; g < G; g++) pk[u].v[g] = (P)popc_of<D>(qs[g], ks[u]);
                 const int ss = s + u * blockDim.x;
-                if (ss < k1) pcs[ss] = pk[u];
+                if (ss >= k1) break;
+                Pack pk;
+#pragma unroll
+                for (int g = 0; g < G; g++) pk.v[g] = (P)popc_of<D>(qs[g], ks[u]);
+                pcs[ss] = pk;
+                count(pk, sk[u]);
             }
-        } else {
+        }
+    } else {
+        // stored popcounts: sixteen keys per thread per iteration
+        constexpr int U = 16;
+        for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
+            Pack pk[U];
+            float sk[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int ss = s + u * blockDim.x;
@@ -128,15 +144,10 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
                 pk[u] = pcs[sc];
                 sk[u] = h2f(a.kb.scales[base + sc]);
             }
-        }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (s + u * (int)blockDim.x >= k1) break;
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const uint32_t key = key_of_pc<D>((int)pk[u].v[g], sk[u]);
-                const bool match = pbits == 0 || (key >> (32 - pbits)) == (pref[g] >> (32 - pbits));
-                if (match) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+            for (int u = 0; u < U; u++) {
+                if (s + u * (int)blockDim.x >= k1) break;
+                count(pk[u], sk[u]);
             }
         }
     }

@@ -41,6 +41,10 @@ CASES = [
     (1, 8, 2, 900, 256, 90, False),     # GQA 4 at d = 256
     (1, 4, 2, 1500, 128, 150, True),    # GQA 2 with ties
     (1, 16, 2, 640, 128, 64, False),    # GQA 8
+    # c5 shape at 8K keys: 512 query heads over 128 KV groups, selection
+    # passes over key chunks of 1024 (several per head), without and with ties
+    (16, 32, 8, 8192, 128, 820, False),
+    (16, 32, 8, 8192, 128, 820, True),
 ]
 
 
