@@ -45,20 +45,20 @@ typedef unsigned int v2u_t __attribute__((ext_vector_type(2)));
 constexpr int kBufWord3 = 0x00020000;
 
 // D/8 sign bytes at byte offset off of a buffer, as D/32 words.
-template <int D>
+template <int D, int AUX>
 __device__ __forceinline__ SignWords<D> buf_signs(__amdgpu_buffer_rsrc_t r, int off) {
     SignWords<D> s;
     if constexpr (D % 128 == 0) {
 #pragma unroll
         for (int i = 0; i < D / 128; i++) {
-            const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+            const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, AUX);
             s.w[4 * i + 0] = v[0]; s.w[4 * i + 1] = v[1]; s.w[4 * i + 2] = v[2]; s.w[4 * i + 3] = v[3];
         }
     } else {
         static_assert(D % 64 == 0, "sign rows of 8-byte multiples");
 #pragma unroll
         for (int i = 0; i < D / 64; i++) {
-            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8 * i, 0, 0);
+            const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8 * i, 0, AUX);
             s.w[2 * i + 0] = v[0]; s.w[2 * i + 1] = v[1];
         }
     }
@@ -81,7 +81,7 @@ struct QDigits {
 // direct loads per array, so reading staging buffer i or the weights does not
 // wait for the direct loads still landing in buffer i+1): V staging buffers
 // (tile i is consumed while tile i+1 lands), each the tile's code bytes then
-// its sign bytes; the (hi, lo) fp16 weight columns [part][2G][64 slots]; the
+// its sign bytes; the (hi, lo) fp16 weight columns [part][2G][72 slots]; the
 // K-side residual dots [64 keys][G] of GQA groups.  The epilogue reduces heads
 // in batches through staging buffer 0.  Binary attention stages no codes.
 template <int D, int G, bool RES>
@@ -91,7 +91,10 @@ struct WaveLds {
     // (lanes 32..63 repeat lanes 0..31 into the second half), hence 1 KB
     static constexpr int kSignBytes = 64 * D / 8 > 1024 ? 64 * D / 8 : 1024;
     static constexpr int kStage = kCodeBytes + kSignBytes;
-    static constexpr int kWeightBytes = 2 * 2 * G * 64 * 2;
+    // weight columns of 72 slots (64 used): the 16 lanes of a row group read
+    // 16-byte runs of 16 columns without LDS bank conflicts
+    static constexpr int kColSlots = 72;
+    static constexpr int kWeightBytes = 2 * 2 * G * kColSlots * 2;
     static constexpr int kRdInts = (G > 1 && RES) ? 64 * G : 4;
     // epilogue: heads per pass through staging buffer 0 ([parts][heads][D] floats)
     static constexpr int kEpiHeads = kStage / ((RES ? 2 : 1) * D * 4) < G ? kStage / ((RES ? 2 : 1) * D * 4) : G;
@@ -203,7 +206,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #define BC_MHA_WAVES 3
 #endif
 #ifndef BC_LIN_K
-#define BC_LIN_K 0
+#define BC_LIN_K 1
 #endif
 #ifndef BC_LIN_V
 #define BC_LIN_V 1
@@ -219,6 +222,16 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #endif
 #ifndef BC_BIN_WAVES
 #define BC_BIN_WAVES 5
+#endif
+// cache policy of the loads that cover whole KiB runs (K and V sign rows, the
+// linear V code tile, the K code blocks of GQA groups, linear K code rows):
+// 2 = nontemporal (measured 8-11% faster; lines that several loads share,
+// like the per-key 16-byte pieces of a code row, keep the default policy)
+#ifndef BC_NT_AUX
+#define BC_NT_AUX 2
+#endif
+#ifndef BC_NT_SCALES
+#define BC_NT_SCALES 0
 #endif
 #ifndef BC_ADAPT_WAVES
 #define BC_ADAPT_WAVES 2
@@ -309,19 +322,25 @@ void attn_mfma_kernel(AttnArgs a) {
     // the key whose score this lane computes (tile-relative)
     const int kown = LIN_K ? (lane % Q) * (64 / Q) + lane / Q : lane;
     const int quarter = lane % Q;
+    // V code tiles of compensated mode (linear rows of CB bytes): the 16-byte
+    // pieces of row k are stored at piece ^ vsw(k), vsw(k) = (k*CB/256) mod Q,
+    // so the rows that one transposed read covers spread over the LDS banks;
+    // the copy permutes the pieces within each row (same cache lines).  A
+    // lane's transposed reads cover row = lane.
+    const int vsw = ((lane * CB) >> 8) & (Q - 1);
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
     const int my_head = my_col >> 1;
     const int bcol = my_col < 2 * G ? my_col : (my_col & 1);
 
-    // weight columns [2 parts][2G cols][64 slots]: this lane's store slot in
+    // weight columns [2 parts][2G cols][72 slots]: this lane's store slot in
     // column 0, and its B-operand read position in column bcol.  The lane
     // offsets go through an opaque copy so that every access is one constant
     // offset from a base that the compiler ties to lds_wts (accesses it cannot
     // tie to one array wait for all direct loads in flight, the prefetch too)
     uint16_t* wsl = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + slot_of(kown));
-    const uint16_t* wrd = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + bcol * 64 + 16 * g4);
+    const uint16_t* wrd = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + bcol * WL::kColSlots + 16 * g4);
     int* rdl = lds_rd[wave];          // [64 keys][G] residual dots
 
     // softmax reference per head, lowered lazily: weights p = 2^(s - m) stay
@@ -439,17 +458,17 @@ void attn_mfma_kernel(AttnArgs a) {
             r.rsv = 0;
             return;
         }
-        r.ks = buf_signs<D>(r_ks, kk * SB);
-        r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
-        r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
+        r.ks = buf_signs<D, BC_NT_AUX>(r_ks, kk * SB);
+        r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, BC_NT_SCALES);
+        r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, BC_NT_SCALES);
         r.rsk = 0;
         r.rsv = 0;
         // residual scales and K codes of every key (adaptive mode too: the
         // selection is known only after the scores, and these loads are the
         // ones worth prefetching; V codes are gathered for selected keys)
         if constexpr (RES) {
-            r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, kk * 2, 0, 0);
-            r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, kk * 2, 0, 0);
+            r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, kk * 2, 0, BC_NT_SCALES);
+            r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, kk * 2, 0, BC_NT_SCALES);
             if constexpr (KMF) {
                 // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
                 const int base = (tr + (lane & 15)) * CB + 16 * (lane >> 4);
@@ -457,7 +476,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                     for (int pc = 0; pc < NPC; pc++) {
-                        const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 16 * kb * CB + 64 * pc, 0, 0);
+                        const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 16 * kb * CB + 64 * pc, 0, BC_NT_AUX);
                         const int i = kb * NPC + pc;
                         r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
                     }
@@ -466,14 +485,15 @@ void attn_mfma_kernel(AttnArgs a) {
                 const int base = LIN_K ? tr * CB + 16 * lane : kk * CB;
 #pragma unroll
                 for (int i = 0; i < Q; i++) {
-                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + (LIN_K ? i * 1024 : 16 * i), 0, 0);
+                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + (LIN_K ? i * 1024 : 16 * i), 0,
+                                                                          LIN_K ? BC_NT_AUX : 0);
                     r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
                 }
             }
         }
     };
-    // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear)
-    // or piece c at c*1024 + 16k (per key)
+    // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear,
+    // pieces swizzled as above) or piece c at c*1024 + 16k (per key)
     auto issue_v = [&](int buf, int t0) {
         const int tr = t0 - key_begin;
         uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
@@ -482,7 +502,7 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
             for (int c = 0; c < SB / 16; c++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs + c * 1024), 16,
-                                                         tr * SB + 16 * lane + c * 1024, 0, 0, 0);
+                                                         tr * SB + 16 * lane + c * 1024, 0, 0, BC_NT_AUX);
         } else {
             // 8-byte rows: one KiB load covers 128 rows, so lanes 32..63 repeat
             // lanes 0..31 (into bytes 512..1023)
@@ -494,7 +514,8 @@ void attn_mfma_kernel(AttnArgs a) {
             for (int c = 0; c < Q; c++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
-                    (LIN_V ? tr * CB + 16 * lane : (tr + lane) * CB) + (LIN_V ? c * 1024 : 16 * c), 0, 0, 0);
+                    LIN_V ? tr * CB + c * 1024 + 16 * (lane ^ ((4 * c + (lane >> 4)) & (Q - 1)))
+                          : (tr + lane) * CB + 16 * c, 0, 0, LIN_V ? BC_NT_AUX : 0);
         }
     };
 
@@ -803,11 +824,11 @@ void attn_mfma_kernel(AttnArgs a) {
             // offset removed at the end, from the unrounded weights: the (hi, lo)
             // pairs carry ~22 bits, so the difference is a zero-mean ~2^-22 term
             off[g] = fmaf(p, fo, off[g]);
-            wsl[(0 * 2 * G + 2 * g) * 64] = a2h;
-            wsl[(0 * 2 * G + 2 * g + 1) * 64] = a2l;
+            wsl[(0 * 2 * G + 2 * g) * WL::kColSlots] = a2h;
+            wsl[(0 * 2 * G + 2 * g + 1) * WL::kColSlots] = a2l;
             if constexpr (RES) {
-                wsl[(1 * 2 * G + 2 * g) * 64] = bh;
-                wsl[(1 * 2 * G + 2 * g + 1) * 64] = bl;
+                wsl[(1 * 2 * G + 2 * g) * WL::kColSlots] = bh;
+                wsl[(1 * 2 * G + 2 * g + 1) * WL::kColSlots] = bl;
             }
         }
         if (any_rescale) {
@@ -839,8 +860,8 @@ void attn_mfma_kernel(AttnArgs a) {
         h8_t bsig[2], bres[2];
 #pragma unroll
         for (int mh = 0; mh < 2; mh++) {
-            bsig[mh] = *(const h8_t*)&wrd[(0 * 2 * G) * 64 + 8 * mh];
-            if constexpr (RES) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * 64 + 8 * mh];
+            bsig[mh] = *(const h8_t*)&wrd[(0 * 2 * G) * WL::kColSlots + 8 * mh];
+            if constexpr (RES) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * WL::kColSlots + 8 * mh];
             else bres[mh] = bsig[mh];
         }
 
@@ -858,7 +879,7 @@ void attn_mfma_kernel(AttnArgs a) {
             if (any_sel) {
 #pragma unroll
                 for (int db = 0; db < NB; db++) {
-                    const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 8 * db
+                    const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 16 * ((db >> 1) ^ vsw) + 8 * (db & 1)
                                               : st_codes + (db >> 1) * 1024 + 16 * row_key + 8 * (db & 1);
                     wrs[db] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, rp));
                 }
