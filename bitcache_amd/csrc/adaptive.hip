@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
             for (int u = 0; u < U; u++) {
                 const int ss = s + u * blockDim.x;
                 const int64_t i = base + (ss < k1 ? ss : s);
-                ks[u] = load_signs<D>(a.kb.signs + i * (D / 8));
+                ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
                 sk[u] = h2f(a.kb.scales[i]);
             }
 #pragma unroll

@@ -490,8 +490,11 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
         for (int i = 0; i < NR; i++) {
             const int key = t0 + i * RPI + row;
             const int64_t ki = base + (key < key_end ? key : t0);
-            kr[i] = ((const uint4*)(K + ki * D))[part];
-            vr[i] = ((const uint4*)(V + ki * D))[part];
+            // nontemporal: each instruction reads whole rows once
+            const bc_v4u kv = __builtin_nontemporal_load((const bc_v4u*)(K + ki * D) + part);
+            const bc_v4u vv = __builtin_nontemporal_load((const bc_v4u*)(V + ki * D) + part);
+            kr[i] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
+            vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
         }
         // scores -> LDS (lane = key)
 #pragma unroll
@@ -637,7 +640,7 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
         for (int u = 0; u < kScoreUnroll; u++) {
             const int s = s0 + u * 256 + (int)threadIdx.x;
             const int64_t ki = base + (s < k1 ? s : k0);        // in range; unused past k1
-            ks[u] = load_signs<D>(kb.signs + ki * (D / 8));
+            ks[u] = load_signs<D, true>(kb.signs + ki * (D / 8));
             sk[u] = h2f(kb.scales[ki]);
         }
 #pragma unroll

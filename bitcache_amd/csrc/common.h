@@ -103,25 +103,30 @@ template <int D>
 struct SignWords {
     uint32_t w[D / 32];
 };
-template <int D>
+typedef unsigned int bc_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int bc_v2u __attribute__((ext_vector_type(2)));
+
+// NT: nontemporal loads (for streams read once, whole lines per instruction)
+template <int D, bool NT = false>
 __device__ __forceinline__ SignWords<D> load_signs(const uint8_t* p) {
     // D/8 bytes at a D/8-byte aligned address: 16-byte loads where the stride allows
     SignWords<D> s;
     if constexpr (D % 128 == 0) {
 #pragma unroll
         for (int i = 0; i < D / 128; i++) {
-            uint4 v = ((const uint4*)p)[i];
-            s.w[4 * i + 0] = v.x; s.w[4 * i + 1] = v.y; s.w[4 * i + 2] = v.z; s.w[4 * i + 3] = v.w;
+            const bc_v4u v = NT ? __builtin_nontemporal_load((const bc_v4u*)p + i) : ((const bc_v4u*)p)[i];
+            s.w[4 * i + 0] = v[0]; s.w[4 * i + 1] = v[1]; s.w[4 * i + 2] = v[2]; s.w[4 * i + 3] = v[3];
         }
     } else if constexpr (D % 64 == 0) {
 #pragma unroll
         for (int i = 0; i < D / 64; i++) {
-            uint2 v = ((const uint2*)p)[i];
-            s.w[2 * i + 0] = v.x; s.w[2 * i + 1] = v.y;
+            const bc_v2u v = NT ? __builtin_nontemporal_load((const bc_v2u*)p + i) : ((const bc_v2u*)p)[i];
+            s.w[2 * i + 0] = v[0]; s.w[2 * i + 1] = v[1];
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < D / 32; i++) s.w[i] = ((const uint32_t*)p)[i];
+        for (int i = 0; i < D / 32; i++)
+            s.w[i] = NT ? __builtin_nontemporal_load((const uint32_t*)p + i) : ((const uint32_t*)p)[i];
     }
     return s;
 }

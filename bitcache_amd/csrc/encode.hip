@@ -168,8 +168,9 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
             const int64_t v = live ? v0 : J.n - 1;
             const int64_t dv = J.row_len == 1 ? v * J.row_stride + J.row_offset
                                               : (v / J.row_len) * J.row_stride + J.row_offset + v % J.row_len;
-            const uint4 raw = ((const uint4*)(J.src + v * D))[j];
-            const uint32_t hw[4] = {raw.x, raw.y, raw.z, raw.w};
+            // nontemporal: the wave's vectors are one contiguous run read once
+            const bc_v4u raw = __builtin_nontemporal_load((const bc_v4u*)(J.src + v * D) + j);
+            const uint32_t hw[4] = {raw[0], raw[1], raw[2], raw[3]};
             float x[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) x[k] = h2f((uint16_t)(hw[k >> 1] >> (16 * (k & 1))));
