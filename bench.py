@@ -281,7 +281,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: every box here has a single MI355X "
-              f"(asked for --gpus {args.gpus}); see DESIGN.md for how the path shards.",
+              f"(asked for --gpus {args.gpus}); the path shards over batch and KV heads, one "
+              f"process per GPU, with no exchange between them.",
               file=sys.stderr)
         sys.exit(2)
     import torch
