@@ -937,8 +937,8 @@ void attn_mfma_kernel(AttnArgs a) {
 
     // ---------------- software-pipelined tile loop: tile i+1 loads in flight
     // while tile i computes (two register sets, two LDS staging buffers).  The
-    // prefetch after a wave's last tile re-reads that tile (harmless, cached)
-    // so that no load sits behind a branch.  Every iteration of the two-tile
+    // prefetch after a wave's last tile addresses the tile past the range: its
+    // loads return zeros and move no data, and no load sits behind a branch.  Every iteration of the two-tile
     // loop starts with no load in flight: the compiler follows direct loads to
     // LDS per staging buffer only within an iteration (across the back edge it
     // would wait for all of them at the first staging-buffer read), so the
@@ -993,13 +993,13 @@ void attn_mfma_kernel(AttnArgs a) {
         issue_v(0, t);
         __builtin_amdgcn_s_waitcnt(0);
         for (;;) {
-            int tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+            int tp = t + 4 * 64;
             load_k(kb, tp);
             issue_v(1, tp);
             process(ka, t, 0);
             t += 4 * 64;
             if (t >= key_end) break;
-            tp = t + 4 * 64 < key_end ? t + 4 * 64 : t;
+            tp = t + 4 * 64;
             load_k(ka, tp);
             issue_v(0, tp);
             process(kb, t, 1);
@@ -1108,8 +1108,9 @@ void launch_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
 namespace bc {
 
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
-    // buffer offsets inside one split's key range are 32-bit
-    if ((int64_t)a.chunk * (D / 2) + 4096 >= ((int64_t)1 << 31)) return false;
+    // buffer offsets are 32-bit and relative to a split's key range; the
+    // prefetches reach up to 12 tiles (768 keys) past its end
+    if (((int64_t)a.chunk + 1024) * (D / 2) + 4096 >= ((int64_t)1 << 31)) return false;
     // adaptive mode reads the popcounts stored by the selection passes
     if (mode == MODE_ADAPTIVE && a.pcs == nullptr) return false;
     switch (D) {
