@@ -4,23 +4,24 @@
 // mapped to an order-preserving uint32 u.  The k-th largest u is found by a
 // radix select over three digits (bits 31..21, 20..10, 9..0): each pass
 // histograms the digit of the keys that still match the prefix found so far
-// (LDS histograms flushed with atomics), and a one-block scan per (b, head)
-// picks the digit where the running count from the top reaches k.  After the
-// third pass the threshold T and the number `need` of keys equal to T that
-// are still to be taken are exact.  Ties at T are taken in key order, i.e.
-// up to a cutoff key index: the third pass also keeps each key chunk's
-// histogram, which locates the chunk holding the need-th tie; one block per
+// (one LDS histogram per key chunk, stored whole), and a one-block scan per
+// (b, head) sums the chunks and picks the digit where the running count from
+// the top reaches k.  After the third pass the threshold T and the number
+// `need` of keys equal to T that are still to be taken are exact.  Ties at T
+// are taken in key order, i.e. up to a cutoff key index: the third pass's
+// chunk histograms locate the chunk holding the need-th tie; one block per
 // (b, head) then scans only that chunk for the cutoff index.  The attention
-// kernel selects key > T, or key == T at an index <= cutoff.
+// kernel selects key > T, or key == T at an index <= cutoff.  Passes, tie
+// scan and attention compare exact float scores against bounds derived from
+// the key prefix (see key_floor), which order like the keys.
 //
 // The first pass computes the popcounts from the K sign planes and stores
 // them (one byte per query head and key; two for d = 256), so the later
 // passes, the tie scan and the attention pass read those instead of the
 // d/8-byte sign rows.
 //
-// Workspace: hist [B*Hq][2048] u32 | prefix [B*Hq] u32 | remain [B*Hq] i32
-//            | cutoff [B*Hq] i32 | chunk histograms [B*Hq][nsplit][1024] u32
-//            | popcounts [B*Hq/G][S][G] | attention partials.
+// Workspace: chunk histograms [B*Hq][nsplit][2048] u32 | prefix [B*Hq] u32
+//            | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G] | attention partials.
 #include "attn.h"
 
 namespace bc {
@@ -43,12 +44,13 @@ struct SelArgs {
     BinPlanes kb;
     int Hq, Hkv, S, kv_stride;
     int nsplit, chunk;   // key chunks of the histogram passes
-    uint32_t* hist;      // [B*Hq][2048]
+    uint32_t* hist;      // [B*Hq][nsplit][2048] each key chunk's histogram of a pass
     uint32_t* prefix;    // [B*Hq]
     int32_t* remain;     // [B*Hq]
     int32_t* cutoff;     // [B*Hq]
-    uint32_t* chist;     // [B*Hq][nsplit][1024] last-pass histogram of each chunk
-    void* pcs;           // [B*Hq/G][S][G] popcounts (PcT<D>)
+    void* pcs;           // [B*Hq/G][pcs_stride(S)][G] popcounts (PcT<D>)
+    int oct;             // K scales load eight keys at a time (kv_stride % 8 == 0,
+                         // 16-byte aligned scale plane)
 };
 
 template <int D, int G>
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
     const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
     const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
-    load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
+    if (pass == 0) load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
     for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) (&h[0][0])[i] = 0u;
     __syncthreads();
     const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
@@ -97,39 +99,167 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
     const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
     using P = PcT<D>;
     using Pack = PcPack<P, G>;
-    Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * a.S;   // this group's [S] packs
-    auto count = [&](const Pack& pk, float sk) {
+    Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S);   // this group's packs
+    // the prefix found so far as a key range [klo, khi] and, for scores of a
+    // finite scale, as the float range (flo, fhi]
+    uint32_t klo[G], khi[G];
+    float flo[G], fhi[G];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const uint32_t key = key_of_pc<D>((int)pk.v[g], sk);
-            const bool match = pbits == 0 || (key >> (32 - pbits)) == (pref[g] >> (32 - pbits));
-            if (match) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+    for (int g = 0; g < G; g++) {
+        const uint32_t low = pbits == 0 ? 0xFFFFFFFFu : (0xFFFFFFFFu >> pbits);
+        klo[g] = pref[g] & ~low;
+        khi[g] = klo[g] | low;
+        flo[g] = klo[g] == 0u ? -INFINITY : key_floor(klo[g] - 1u);
+        fhi[g] = key_floor(khi[g]);
+    }
+    // one key: the popcounts pc[g] of the G heads and the K scale
+    auto count_key = [&](const int* pc, float sk, bool all) {
+        // (a wave with a non-finite scale takes the key path for all its lanes)
+        if (__ballot(!finite_scale(sk)) == 0ull) {
+            const float sk2 = 2.0f * sk, nd = -(float)D * sk;
+            float sc[G];
+            bool mt[G];
+            bool any = false;
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                sc[g] = fmaf((float)pc[g], sk2, nd);
+                mt[g] = all || (sc[g] > flo[g] && sc[g] <= fhi[g]);
+                any = any || mt[g];
+            }
+            // (later passes: most waves have no match for a key, and skip it)
+            if (all || __ballot(any) != 0ull) {
+#pragma unroll
+                for (int g = 0; g < G; g++)
+                    if (mt[g]) atomicAdd(&h[g][(ordered_bits(sc[g]) >> shift) & dmask], 1u);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const uint32_t key = key_of_pc<D>(pc[g], sk);
+                if (key >= klo[g] && key <= khi[g]) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+            }
         }
     };
+    auto count = [&](const Pack& pk, float sk, bool all) {
+        int pc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) pc[g] = (int)pk.v[g];
+        count_key(pc, sk, all);
+    };
     if (pass == 0) {
-        // popcounts from the sign rows, stored for the later passes; eight
-        // keys per thread per iteration, all loads issued first
-        constexpr int U = 8;
-        for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
-            SignWords<D> ks[U];
-            float sk[U];
+        // popcounts from the sign rows, stored for the later passes.  Two
+        // register stages of UP keys per thread: the loads of the next stage
+        // are in flight while a stage is counted.
+        constexpr int UP = D >= 256 ? 2 : 4;
+        constexpr int step = UP * 256;
+        struct Stage {
+            SignWords<D> ks[UP];
+            uint16_t sk[UP];
+        };
+        auto load = [&](Stage& st, int s) {
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int ss = s + u * blockDim.x;
-                const int64_t i = base + (ss < k1 ? ss : s);
-                ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
-                sk[u] = h2f(a.kb.scales[i]);
+            for (int u = 0; u < UP; u++) {
+                const int ss = s + u * 256;
+                const int64_t i = base + (ss < k1 ? ss : k0);
+                st.ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
+                st.sk[u] = a.kb.scales[i];
             }
+        };
+        auto run = [&](const Stage& st, int s) {
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int ss = s + u * blockDim.x;
+            for (int u = 0; u < UP; u++) {
+                const int ss = s + u * 256;
                 if (ss >= k1) break;
                 Pack pk;
 #pragma unroll
-                for (int g = 0; g < G; g++) pk.v[g] = (P)popc_of<D>(qs[g], ks[u]);
+                for (int g = 0; g < G; g++) pk.v[g] = (P)popc_of<D>(qs[g], st.ks[u]);
                 pcs[ss] = pk;
-                count(pk, sk[u]);
+                count(pk, h2f(st.sk[u]), true);
             }
+        };
+        if (k0 + (int)threadIdx.x < k1) {
+            Stage sa, sb;
+            int s = k0 + threadIdx.x;
+            load(sa, s);
+            for (;;) {
+                load(sb, s + step);
+                run(sa, s);
+                s += step;
+                if (s >= k1) break;
+                load(sa, s + step);
+                run(sb, s);
+                s += step;
+                if (s >= k1) break;
+            }
+        }
+    } else if (a.oct) {
+        // stored popcounts, eight consecutive keys per lane and load: their
+        // packs (8 G-head packs, whole 16-byte loads where they fill one) and
+        // their K scales (16 bytes).  Two register stages of UP octets: the
+        // loads of the next stage are in flight while a stage is counted.
+        constexpr int kOct = 8 * (int)sizeof(Pack);   // pack bytes of eight keys
+        constexpr int NW = kOct / 4;
+        constexpr int UP = kOct >= 64 ? 1 : 2;         // octets per lane and stage
+        constexpr int step = UP * 256;                 // octets per block and stage
+        const int o0 = k0 / 8, o1 = (k1 + 7) / 8;
+        const uint16_t* scales = a.kb.scales + base;
+        struct Stage {
+            uint32_t pw[UP][NW];
+            bc_v4u sc[UP];
+        };
+        auto load = [&](Stage& st, int o) {
+#pragma unroll
+            for (int u = 0; u < UP; u++) {
+                const int oo = o + u * 256;
+                const int oc = oo < o1 ? oo : o0;
+                const uint32_t* src = (const uint32_t*)(pcs + 8 * oc);
+                if constexpr (kOct >= 16) {
+#pragma unroll
+                    for (int v = 0; v < kOct / 16; v++) {
+                        const bc_v4u x = ((const bc_v4u*)src)[v];
+                        st.pw[u][4 * v] = x[0]; st.pw[u][4 * v + 1] = x[1];
+                        st.pw[u][4 * v + 2] = x[2]; st.pw[u][4 * v + 3] = x[3];
+                    }
+                } else {
+                    const bc_v2u x = *(const bc_v2u*)src;
+                    st.pw[u][0] = x[0]; st.pw[u][1] = x[1];
+                }
+                st.sc[u] = *(const bc_v4u*)(scales + 8 * oc);
+            }
+        };
+        auto run = [&](const Stage& st, int o) {
+#pragma unroll
+            for (int u = 0; u < UP; u++) {
+                const int oo = o + u * 256;
+                if (oo >= o1) break;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (8 * oo + j >= k1) break;   // (only the range's last octet is partial)
+                    const uint32_t sw = st.sc[u][j >> 1];
+                    const float sk = h2f((uint16_t)((j & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+                    int pc[G];
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        constexpr int pb = (int)sizeof(P);
+                        const int byte = (j * G + g) * pb;
+                        pc[g] = (int)((st.pw[u][byte / 4] >> (8 * (byte % 4))) & ((1u << (8 * pb)) - 1u));
+                    }
+                    count_key(pc, sk, false);
+                }
+            }
+        };
+        Stage sa, sb;
+        int o = o0 + threadIdx.x;
+        load(sa, o);
+        for (;;) {
+            load(sb, o + step);
+            run(sa, o);
+            o += step;
+            if (o >= o1) break;
+            load(sa, o + step);
+            run(sb, o);
+            o += step;
+            if (o >= o1) break;
         }
     } else {
         // stored popcounts: sixteen keys per thread per iteration
@@ -147,32 +277,43 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 if (s + u * (int)blockDim.x >= k1) break;
-                count(pk[u], sk[u]);
+                count(pk[u], sk[u], false);
             }
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) {
-        const uint32_t c = (&h[0][0])[i];
-        const int g = i / kBins, bin = i % kBins;
-        if (c) atomicAdd(&a.hist[(int64_t)(bhq0 + g) * kBins + bin], c);
-        if (pass == 2 && bin < 1024)
-            a.chist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * 1024 + bin] = c;
+    // this chunk's histogram, stored whole (plain coalesced stores; the pick
+    // sums the chunks, and the last pass's chunk histograms locate the ties)
+    const int nb = pass == 2 ? 1024 : kBins;
+    for (int i = threadIdx.x; i < G * nb; i += blockDim.x) {
+        const int g = i / nb, bin = i % nb;
+        a.hist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * kBins + bin] = h[g][bin];
     }
 }
 
-// One block per (b, query head): pick the digit holding the remain-th largest
-// key, extend the prefix, and clear the histogram for the next pass.
+// One block per (b, query head): sum the chunk histograms of the pass and
+// pick the digit holding the remain-th largest key; extend the prefix.
 __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_k) {
     __shared__ uint32_t cnt[kBins];
     __shared__ uint32_t part[256];
     const int bhq = blockIdx.x;
-    uint32_t* h = a.hist + (int64_t)bhq * kBins;
+    const uint32_t* h = a.hist + (int64_t)bhq * a.nsplit * kBins;
     const int nbins = pass == 2 ? 1024 : 2048;
     const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    for (int i = threadIdx.x; i < kBins; i += blockDim.x) {
-        cnt[i] = h[i];
-        h[i] = 0u;
+    {
+        // eight consecutive bins per thread (the last pass stores 1024)
+        const int b0 = threadIdx.x * 8;
+        uint32_t sum[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if (b0 < nbins) {
+            for (int c = 0; c < a.nsplit; c++) {
+                const bc_v4u x = *(const bc_v4u*)(h + (int64_t)c * kBins + b0);
+                const bc_v4u y = *(const bc_v4u*)(h + (int64_t)c * kBins + b0 + 4);
+                sum[0] += x[0]; sum[1] += x[1]; sum[2] += x[2]; sum[3] += x[3];
+                sum[4] += y[0]; sum[5] += y[1]; sum[6] += y[2]; sum[7] += y[3];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) cnt[b0 + j] = sum[j];
     }
     __syncthreads();
     int remain = pass == 0 ? top_k : a.remain[bhq];
@@ -244,11 +385,12 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
         return;
     }
     const uint32_t T = a.prefix[bhq];
+    const float tv = key_value(T);   // the score of key T (finite scales)
     if (threadIdx.x == 0) {
-        const uint32_t* ch = a.chist + (int64_t)bhq * a.nsplit * 1024 + (T & 0x3FFu);
+        const uint32_t* ch = a.hist + (int64_t)bhq * a.nsplit * kBins + (T & 0x3FFu);
         int cum = 0, c = 0;
         for (; c < a.nsplit - 1; c++) {
-            const int t = (int)ch[(int64_t)c * 1024];
+            const int t = (int)ch[(int64_t)c * kBins];
             if (cum + t >= need) break;
             cum += t;
         }
@@ -257,7 +399,7 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     }
     __syncthreads();
     const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
-    const Pack* pcs = (const Pack*)a.pcs + (int64_t)(bhq - g) / G * a.S;
+    const Pack* pcs = (const Pack*)a.pcs + (int64_t)(bhq - g) / G * bc::pcs_stride(a.S);
     const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
     // windows of 64 stripes of 256 keys, read coalesced (all loads of 16
     // stripes issued first); a wave ballot per stripe records the ties; one
@@ -279,7 +421,11 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
 #pragma unroll
             for (int u = 0; u < 16; u++) {
                 const int sv = w0 + (b0 + u) * 256 + (int)threadIdx.x;
-                const uint64_t m = __ballot(sv < k1 && key_of_pc<D>(pcv[u], skv[u]) == T);
+                const float sk = skv[u];
+                bool tie;
+                if (__ballot(!finite_scale(sk)) == 0ull) tie = fmaf((float)pcv[u], 2.0f * sk, -(float)D * sk) == tv;
+                else tie = key_of_pc<D>(pcv[u], sk) == T;
+                const uint64_t m = __ballot(sv < k1 && tie);
                 if (lane == 0) tmask[b0 + u][wave] = m;
             }
         }
@@ -319,11 +465,6 @@ __global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
     }
 }
 
-__global__ void zero_kernel(uint32_t* p, int64_t n) {
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
-}
-
 int pick_g(int group) {
     if (group % 8 == 0) return 8;
     if (group % 4 == 0) return 4;
@@ -352,7 +493,7 @@ Chunks chunks_for(int batch, int hq, int hkv, int S) {
 }
 
 struct Layout {
-    size_t hist, prefix, remain, cutoff, chist, pcs, attn, total;
+    size_t hist, prefix, remain, cutoff, pcs, attn, total;
 };
 
 Layout layout(int batch, int hq, int hkv, int S, int d) {
@@ -361,12 +502,11 @@ Layout layout(int batch, int hq, int hkv, int S, int d) {
     const Chunks c = chunks_for(batch, hq, hkv, S);
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.hist = 0;
-    L.prefix = al(L.hist + bh * kBins * 4);
+    L.prefix = al(L.hist + bh * (size_t)c.nsplit * kBins * 4);
     L.remain = al(L.prefix + bh * 4);
     L.cutoff = al(L.remain + bh * 4);
-    L.chist = al(L.cutoff + bh * 4);
-    L.pcs = al(L.chist + bh * (size_t)c.nsplit * 1024 * 4);
-    L.attn = al(L.pcs + bh * (size_t)S * (d > 255 ? 2 : 1));
+    L.pcs = al(L.cutoff + bh * 4);
+    L.attn = al(L.pcs + bh * (size_t)bc::pcs_stride(S) * (d > 255 ? 2 : 1));
     L.total = L.attn + bc::attention_ws_bytes(batch, hq, hkv, S, d);
     return L;
 }
@@ -437,12 +577,8 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     a.prefix = (uint32_t*)(ws + L.prefix);
     a.remain = (int32_t*)(ws + L.remain);
     a.cutoff = (int32_t*)(ws + L.cutoff);
-    a.chist = (uint32_t*)(ws + L.chist);
     a.pcs = ws + L.pcs;
-    // clear the histograms with a kernel (no memset nodes: graph-capture safe)
-    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, a.hist, (int64_t)bh * kBins);
-    int rc = bc::check_launch("adaptive zero");
-    if (rc != BC_OK) return rc;
+    a.oct = kv_stride % 8 == 0 && ((uintptr_t)a.kb.scales % 16) == 0;
     const int G = pick_g(n_heads / n_kv_heads);
     const int groups = batch * n_kv_heads * ((n_heads / n_kv_heads) / G);
     const Chunks c = chunks_for(batch, n_heads, n_kv_heads, seq_len);
@@ -461,7 +597,7 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
         case 256: run_passes_g<256>(G, a, groups, chunk, nsplit, bh, k, st); break;
         default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
     }
-    rc = bc::check_launch("adaptive select");
+    int rc = bc::check_launch("adaptive select");
     if (rc != BC_OK) return rc;
     return bc::run_attention(2, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
                              seq_len, kv_stride, head_dim, ws + L.attn, workspace_bytes - L.attn,

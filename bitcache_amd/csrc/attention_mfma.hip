@@ -375,11 +375,14 @@ void attn_mfma_kernel(AttnArgs a) {
 
     uint32_t thresh[G];
     int cutoff[G];
+    float thr_floor[G], thr_value[G];   // the threshold as float bounds
     if constexpr (MODE == MODE_ADAPTIVE) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             thresh[g] = a.thresh[bhq0 + g];
             cutoff[g] = a.cutoff[bhq0 + g];
+            thr_floor[g] = key_floor(thresh[g]);
+            thr_value[g] = key_value(thresh[g]);
         }
     }
 
@@ -427,7 +430,7 @@ void attn_mfma_kernel(AttnArgs a) {
     constexpr int kPack = (int)sizeof(Pack);
     static_assert(kPack <= 16, "one load per pack");
     const __amdgpu_buffer_rsrc_t r_pc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const Pack*)a.pcs + (int64_t)bhq0 / G * a.S + key_begin), (short)0, nk * kPack, kBufWord3);
+        (void*)((const Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S) + key_begin), (short)0, nk * kPack, kBufWord3);
     // an offset past every range (the host keeps each range's bytes below
     // 2^31 - 4096): such a load returns zeros and moves no data
     constexpr int kOob = 0x7FFFF000;
@@ -529,15 +532,27 @@ void attn_mfma_kernel(AttnArgs a) {
         const bool valid = s < key_end;
         const float sk = h2f(r.sk);
         uint32_t selmask = 0;
+        // selected: above the threshold, or equal to it at an index up to the
+        // cutoff (ties are taken lowest index first); compared as exact float
+        // scores unless a lane of the wave has a non-finite scale
+        const bool fast = __ballot(!finite_scale(sk)) == 0ull;
+        const float sk2 = 2.0f * sk, nd = -(float)D * sk;
 #pragma unroll
         for (int g = 0; g < G; g++) {
             constexpr int bits = 8 * (int)sizeof(bc::PcT<D>);
             constexpr int per_word = 32 / bits;
             const int pc = (int)((r.pcw[g / per_word] >> (bits * (g % per_word))) & ((1u << bits) - 1u));
-            // selected: above the threshold, or equal to it at an index up to
-            // the cutoff (ties are taken lowest index first)
-            const uint32_t key = ordered_key(sk * (float)(2 * pc - D));
-            const bool sel = key > thresh[g] || (key == thresh[g] && s <= cutoff[g]);
+            bool above, tie;
+            if (fast) {
+                const float sc = fmaf((float)pc, sk2, nd);
+                above = sc > thr_floor[g];
+                tie = sc == thr_value[g];
+            } else {
+                const uint32_t key = ordered_key(sk * (float)(2 * pc - D));
+                above = key > thresh[g];
+                tie = key == thresh[g];
+            }
+            const bool sel = above || (tie && s <= cutoff[g]);
             selmask |= (sel && valid) ? (1u << g) : 0u;
         }
         r.sel = selmask;

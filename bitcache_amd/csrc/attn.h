@@ -22,9 +22,14 @@ struct AttnArgs {
     const int32_t* cutoff;       // [B*Hq] keys equal to the threshold are taken up to
                                  // this key index (-1: none)
     uint8_t* selected;           // optional [B, Hq, S]
-    const void* pcs;             // adaptive: [B*Hq/G][S] PcPack<PcT<D>, G> popcounts of
-                                 // the selection passes (G = the kernel's head group)
+    const void* pcs;             // adaptive: [B*Hq/G][pcs_stride(S)] PcPack<PcT<D>, G>
+                                 // popcounts of the selection passes (G = the kernel's
+                                 // head group)
 };
+
+// Packs per row of the stored popcounts: S rounded up to 16, so that every
+// row starts 16-byte aligned and eight-key runs load whole.
+__host__ __device__ inline int pcs_stride(int S) { return (S + 15) & ~15; }
 
 // Stored popcount of one (query head, key): 8 bits, 16 for d = 256 (popcount
 // up to 256).  A pack holds the G heads of a query-head group for one key.

@@ -140,3 +140,29 @@ __device__ __forceinline__ uint32_t ordered_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Ranking scores of the top-k selection in the float domain.  For a finite
+// scale, fma(pc, 2 scale, -d scale) is exactly scale * (2pc - d) (at most 20
+// significant bits), never -0 and never NaN; on such scores the order of
+// ordered_key() is the float order, so a bound on keys is a float bound:
+//   ordered_key(s) <= T  <=>  s <= key_floor(T)
+//   ordered_key(s) == T  <=>  s == key_value(T)   (NaN: no such score)
+// key_floor(T) is the largest float that is not -0 or NaN whose key is <= T
+// (-inf when there is none, since every such score is finite).
+__host__ __device__ inline float key_floor(uint32_t T) {
+    if (T >= 0xFF800000u) return INFINITY;    // the key of +inf, or a NaN's
+    if (T < 0x007FFFFFu) return -INFINITY;    // below the key of -inf (NaNs)
+    const uint32_t bits = (T & 0x80000000u) ? (T & 0x7FFFFFFFu) : ~T;
+    // -0 never occurs: the next float below it
+    return __builtin_bit_cast(float, bits == 0x80000000u ? 0x80000001u : bits);
+}
+__host__ __device__ inline float key_value(uint32_t T) {
+    if (T > 0xFF800000u || T < 0x007FFFFFu || T == 0x7FFFFFFFu) return __builtin_nanf("");
+    return __builtin_bit_cast(float, (T & 0x80000000u) ? (T & 0x7FFFFFFFu) : ~T);
+}
+// ordered_key() of a score that is not NaN or -0 (no folding needed)
+__device__ __forceinline__ uint32_t ordered_bits(float s) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, s);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ bool finite_scale(float sk) { return __builtin_fabsf(sk) < INFINITY; }
+
