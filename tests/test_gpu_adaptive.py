@@ -112,3 +112,34 @@ def test_config_c5_sample(F):
     for (b, h), idx in sets.items():
         assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"set differs at {(b, h)}"
     close(to_np(out).astype(np.float32), ref, what="c5 sample")
+
+
+def test_adaptive_special_scales(F):
+    """Selected sets with planted K scales: +-inf, NaN, +-0, negative, the
+    fp16 maximum and a subnormal.  Waves holding a non-finite scale rank by the
+    exact key, the others by exact float scores; both must give the oracle's
+    order (NaN below every key, -0 as +0, ties lowest index first).  Only the
+    sets are compared: non-finite scales make the outputs non-finite."""
+    say("case adaptive special scales")
+    B, Hq, Hkv, S, d, k = 1, 8, 2, 2048, 128, 300
+    q, kx, vx = make(B, Hq, Hkv, S, d, seed=11)
+    kb, kr = F.encode_fused(torch.from_numpy(kx.reshape(-1, d)).cuda())
+    vb, vr = F.encode_fused(torch.from_numpy(vx.reshape(-1, d)).cuda())
+    n = B * Hkv * S
+    scales = kb[n * d // 8:n * d // 8 + 2 * n].view(torch.float16)
+    rng = np.random.default_rng(12)
+    special = [np.inf, -np.inf, np.nan, 0.0, -0.0, -0.05, 65504.0, 6e-8, 0.5, 0.5]
+    pos = rng.choice(n, size=60, replace=False)
+    vals = torch.tensor([special[i % len(special)] for i in range(len(pos))], dtype=torch.float16)
+    scales[torch.from_numpy(pos).cuda()] = vals.cuda()
+    torch.cuda.synchronize()
+    out, sel = F.adaptive_attention(torch.from_numpy(q).cuda(), kb, kr, vb, vr, B, Hq, S, d,
+                                    n_kv_heads=Hkv, top_k=k, return_selected=True)
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    with np.errstate(all="ignore"):
+        _, _, sets = O.adaptive_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, k, n_kv_heads=Hkv,
+                                          return_f32=True, return_sets=True)
+    sel = to_np(sel)
+    for (b, h), idx in sets.items():
+        assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"set differs at {(b, h)}"
