@@ -740,30 +740,57 @@ struct SplitPlan {
     int n_splits, chunk, G;
 };
 
-SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
+// Key splits per (b, query-head group).  per_cu > 0: the launch is modelled
+// as rounds of `per_cu` resident workgroups per CU, a split count s costing
+// rounds(s) * (tiles per split + 2), the 2 standing for a workgroup's fixed
+// prologue/epilogue/combine cost in tiles; the cheapest s wins (the fewer
+// splits on a tie), so a launch that fits is one round of equal workgroups
+// and no CU idles at its tail (measured faster on the c2, c4 and c5 shapes).
+// per_cu = 0: about 8 workgroups per CU, i.e. several rounds that balance
+// per-CU speed differences of a long bandwidth-bound launch (measured faster
+// on the 64K-context MHA compensated step); a launch too small for two such
+// rounds fills one round of 3 workgroups per CU.
+SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
     SplitPlan p;
     p.G = pick_g(hq / hkv);
-    const int groups = batch * hkv * ((hq / hkv) / p.G);
+    const int64_t groups = (int64_t)batch * hkv * ((hq / hkv) / p.G);
     const int tiles = (S + 63) / 64;
     const int cu = bc::device_cu_count();
-    // ~8 workgroups per CU: several rounds of 2-3 resident workgroups per CU keep
-    // the tail of the launch short (measured on the 64K-context MHA step).  A
-    // launch too small for two such rounds instead fills exactly one round of
-    // 3 workgroups per CU (measured on the 16K-context GQA decode step).
-    int want = (8 * cu + groups - 1) / groups;
     int max_split = tiles / 8;                   // at least 8 tiles (2 per wave) per split
+    if (max_split > kMaxSplits) max_split = kMaxSplits;   // the combine kernel's weight table
     if (max_split < 1) max_split = 1;
-    if (want > max_split) want = max_split;
-    if ((int64_t)groups * want < 6LL * cu) {
-        const int one_round = (3 * cu) / (groups > 0 ? groups : 1);
-        want = one_round < max_split ? one_round : max_split;
+    int want = 1;
+    if (groups > 0 && tiles > 0 && per_cu > 0) {
+        const int64_t slots = (int64_t)per_cu * cu;
+        // beyond 4 rounds' worth of splits nothing improves
+        const int64_t lim = 4 * slots / groups + 1;
+        const int hi = lim < max_split ? (int)lim : max_split;
+        double best = 0.0;
+        for (int sp = 1; sp <= hi; sp++) {
+            const int per = (tiles + sp - 1) / sp;
+            const int n = (tiles + per - 1) / per;
+            if (n != sp) continue;               // (the same plan as a smaller count)
+            const int64_t rounds = (groups * n + slots - 1) / slots;
+            const double t = (double)rounds * (per + 2);
+            if (sp == 1 || t < best * 0.999) {
+                best = t;
+                want = sp;
+            }
+        }
+    } else if (groups > 0) {
+        want = (int)((8 * cu + groups - 1) / groups);
+        if (want > max_split) want = max_split;
+        if (groups * want < 6LL * cu) {
+            const int64_t one_round = (3LL * cu) / groups;
+            want = one_round < max_split ? (int)one_round : max_split;
+        }
     }
     static const int forced = [] {
         const char* e = getenv("BITCACHE_SPLITS");
         return e ? atoi(e) : 0;
     }();
     if (forced > 0) want = forced < tiles ? forced : tiles;   // tuning override
-    if (want > kMaxSplits) want = kMaxSplits;   // the combine kernel's weight table
+    if (want > kMaxSplits) want = kMaxSplits;
     if (want < 1) want = 1;
     const int tiles_per = (tiles + want - 1) / want;
     p.chunk = tiles_per * 64;
@@ -771,9 +798,29 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S) {
     return p;
 }
 
+// The split policy of a full attention call (plan_splits' per_cu): MHA
+// compensated attention several rounds; binary and GQA compensated attention
+// one round of three workgroups per CU; adaptive attention one round of what
+// fits (its LDS allows two workgroups per CU at d = 128), at most three.
+int plan_per_cu(int mode, int D, int G) {
+    if (mode == MODE_COMP && G == 1) return 0;
+    if (mode != MODE_ADAPTIVE) return 3;
+    const int n = bc::mfma_wgs_per_cu(mode, D, G);
+    return n <= 0 ? 3 : (n < 3 ? n : 3);
+}
+// the policy of the split-phase entry points (bc_attention_partial and
+// bc_attention_combine, which does not know the mode), and of the fp16
+// reference kernel
+constexpr int kPlanFixed = 0;
+
+// workspace of the split partials: the largest plan of any mode
 size_t ws_bytes(int batch, int hq, int hkv, int S, int D) {
-    SplitPlan p = plan_splits(batch, hq, hkv, S);
-    return (size_t)batch * hq * p.n_splits * (D + 2) * sizeof(float);
+    int n = 1;
+    for (int per_cu = 0; per_cu <= 3; per_cu++) {
+        const SplitPlan p = plan_splits(batch, hq, hkv, S, per_cu);
+        n = p.n_splits > n ? p.n_splits : n;
+    }
+    return (size_t)batch * hq * n * (D + 2) * sizeof(float);
 }
 
 int validate_heads(int batch, int n_heads, int n_kv_heads, int seq_len, int kv_stride, int d) {
@@ -837,7 +884,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
                 const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
                 hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
-                uint8_t* selected, const void* pcs) {
+                uint8_t* selected, const void* pcs, int per_cu) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -847,7 +894,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
     BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
                "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
-    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu);
     const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
     AttnArgs a{};
     a.q = (const uint16_t*)q;
@@ -880,13 +927,13 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     return bc::check_launch("attention split");
 }
 
-int run_combine(const void* workspace, void* out, int batch, int n_heads, int n_kv_heads,
+int run_combine(int per_cu, const void* workspace, void* out, int batch, int n_heads, int n_kv_heads,
                 int seq_len, int head_dim, hipStream_t st) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
     BC_REQUIRE(workspace && out, BC_ERR_INVALID_ARGUMENT, "null pointer");
-    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu);
     BC_DISPATCH_D(head_dim, launch_combine, (const float*)workspace, (uint16_t*)out,
                   batch * n_heads, p.n_splits, st);
     return bc::check_launch("attention combine");
@@ -897,13 +944,15 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
                   const int32_t* cutoff, uint8_t* selected, const void* pcs) {
+    const int per_cu = head_dim > 0 && n_kv_heads > 0
+                           ? plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads)) : kPlanFixed;
     int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
                          kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
-                         selected, pcs);
+                         selected, pcs, per_cu);
     if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
-    return run_combine(workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim, st);
+    return run_combine(per_cu, workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim, st);
 }
 
 size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d) {
@@ -929,12 +978,14 @@ extern "C" int bc_attention_partial(const void* q, const void* k_bin, const void
                "k_res and v_res must both be given or both be null");
     return bc::run_partial(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, batch,
                            n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
-                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr,
+                           kPlanFixed);
 }
 
 extern "C" int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads,
                                     int n_kv_heads, int seq_len, int head_dim, void* stream) {
-    return bc::run_combine(workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim,
+    // (the partials of bc_attention_partial, planned with the same fixed policy)
+    return bc::run_combine(kPlanFixed, workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim,
                            (hipStream_t)stream);
 }
 
@@ -1051,7 +1102,7 @@ extern "C" int bc_reference_attention(const void* q, const void* k, const void* 
     const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
     BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
                "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
-    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len);
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, kPlanFixed);
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {

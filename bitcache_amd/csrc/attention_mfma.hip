@@ -24,6 +24,10 @@
 
 #include "attn.h"
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 using bc::AttnArgs;
 using bc::kLog2e;
 using bc::MODE_ADAPTIVE;
@@ -1118,9 +1122,52 @@ void launch_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
     }
 }
 
+template <int D, int G>
+int occupancy_dg(int mode) {
+    int n = 0;
+    hipError_t e;
+    if (mode == MODE_BINARY)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_BINARY>, 256, 0);
+    else if (mode == MODE_COMP)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_COMP>, 256, 0);
+    else
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_ADAPTIVE>, 256, 0);
+    return e == hipSuccess ? n : 0;
+}
+
+template <int D>
+int occupancy_d(int mode, int G) {
+    switch (G) {
+        case 8: return occupancy_dg<D, 8>(mode);
+        case 4: return occupancy_dg<D, 4>(mode);
+        case 2: return occupancy_dg<D, 2>(mode);
+        default: return occupancy_dg<D, 1>(mode);
+    }
+}
+
 }  // namespace
 
 namespace bc {
+
+int mfma_wgs_per_cu(int mode, int D, int G) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int, int>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    const auto key = std::make_tuple(dev, mode, D, G);
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    switch (D) {
+        case 64: n = occupancy_d<64>(mode, G); break;
+        case 128: n = occupancy_d<128>(mode, G); break;
+        case 256: n = occupancy_d<256>(mode, G); break;
+        default: n = 0;
+    }
+    cache[key] = n;
+    return n;
+}
 
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
     // buffer offsets are 32-bit and relative to a split's key range; the

@@ -44,4 +44,7 @@ struct __attribute__((aligned(G * sizeof(P)))) PcPack {
 // MFMA value-phase kernels (attention_mfma.hip): true if (D, G, mode) is
 // handled there and the launch was issued.
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st);
+// Resident workgroups per CU of the MFMA kernel of (mode, D, G) on the current
+// device (0 when no MFMA kernel handles it).
+int mfma_wgs_per_cu(int mode, int D, int G);
 }  // namespace bc
