@@ -1054,24 +1054,38 @@ void attn_mfma_kernel(AttnArgs a) {
         const int hs = my_head - g0;   // this lane's head slot in the batch
         const bool wr = writer && hs >= 0 && hs < HP;
         if (g0 > 0) __syncthreads();   // the previous batch has been read
+        // hi + lo: the neighbour lane's column by DPP (quad_perm [1,0,3,2]),
+        // all sums first, then the stores under one branch
+        float sv[NH][4][4];
+        float nv[RES ? NB : 1][4];
 #pragma unroll
         for (int h = 0; h < NH; h++)
 #pragma unroll
             for (int p = 0; p < 4; p++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < 4; i++)
                     // accumulator p carries 2^p (bit p read in place)
-                    const float v = (cs[h][p][i] + __shfl_xor(cs[h][p][i], 1, 64)) * (1.0f / (float)(1 << p));
-                    if (wr) accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = v;
-                }
+                    sv[h][p][i] = (cs[h][p][i] + dpp_f<0xB1>(cs[h][p][i])) * (1.0f / (float)(1 << p));
         if constexpr (RES) {
 #pragma unroll
             for (int d = 0; d < NB; d++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float v = cn[d][i] + __shfl_xor(cn[d][i], 1, 64);
-                    if (wr) accw[(1 * HP + hs) * D + 16 * d + 4 * g4 + i] = v;
-                }
+                for (int i = 0; i < 4; i++) nv[d][i] = cn[d][i] + dpp_f<0xB1>(cn[d][i]);
+        }
+        if (wr) {
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+#pragma unroll
+                for (int p = 0; p < 4; p++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = sv[h][p][i];
+            if constexpr (RES) {
+#pragma unroll
+                for (int d = 0; d < NB; d++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) accw[(1 * HP + hs) * D + 16 * d + 4 * g4 + i] = nv[d][i];
+            }
         }
         __syncthreads();
         const int nh = min(HP, G - g0);
