@@ -133,10 +133,25 @@ __device__ __forceinline__ int slot_of(int k) {
     return 16 * g4 + 8 * mh + ((r & 3) << 1) + (r >> 2);
 }
 
+// Query preparation of one workgroup (256 threads), spread over all threads:
+// the query as floats and its sign words (a wave ballot per 64 elements);
+// scale_q (sequential fp32 order, element 0 first) and the fixed-point step dq
+// per head; q_int = rint(q / dq) per element; then the balanced int4 digit
+// words (one (word, digit) pair per thread) and the int8 MFMA operand words.
 template <int D, int G, bool KMF>
 __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf) {
-    const int tid = threadIdx.x;
-    for (int i = tid; i < G * D; i += blockDim.x) qf[i] = h2f(qbase[i]);
+    static_assert((G * D) % 64 == 0, "whole waves of query elements");
+    const int tid = threadIdx.x, lane = tid & 63;
+    uint32_t* signs = &qd.signs[0][0];   // [G * D / 32] words, bit b of word i = element 32i + b
+    for (int i = tid; i < G * D; i += 256) {
+        const float x = h2f(qbase[i]);
+        qf[i] = x;
+        const uint64_t bits = __ballot(x >= 0.0f);
+        if (lane == 0) {
+            signs[i / 32] = (uint32_t)bits;
+            signs[i / 32 + 1] = (uint32_t)(bits >> 32);
+        }
+    }
     __syncthreads();
     if (tid < G) {
         // sequential fp32 order (element 0 first); the reads are independent
@@ -152,35 +167,38 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         // |q_int| <= 30583 keeps the top digit in [-8, 7]
         qd.dq[tid] = mx > 0.0f ? mx / 30583.0f : 1.0f;
     }
-    for (int i = tid; i < G * (D / 32); i += blockDim.x) {
-        const int g = i / (D / 32), w = i % (D / 32);
-        uint32_t bits = 0;
-        for (int b = 0; b < 32; b++) bits |= (qf[g * D + 32 * w + b] >= 0.0f ? 1u : 0u) << b;
-        qd.signs[g][w] = bits;
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D;
+        qd.qint[g][i % D] = (int16_t)(int)__builtin_rintf(qf[i] / qd.dq[g]);
     }
     __syncthreads();
-    for (int i = tid; i < G * (D / 8); i += blockDim.x) {
-        const int g = i / (D / 8), w = i % (D / 8);
-        uint32_t dg[4] = {0u, 0u, 0u, 0u};
+    // digit j of the 8 elements of word w: nibble k = element 8w + k (balanced
+    // base 16: t = sum_j d_j 16^j, d_j in [-8, 7])
+    for (int e = tid; e < G * (D / 8) * 4; e += 256) {
+        const int j = e & 3, gw = e >> 2, g = gw / (D / 8), w = gw % (D / 8);
+        uint32_t word = 0u;
+#pragma unroll
         for (int k = 0; k < 8; k++) {
-            int t = (int)__builtin_rintf(qf[g * D + 8 * w + k] / qd.dq[g]);
-            qd.qint[g][8 * w + k] = (int16_t)t;
-            for (int j = 0; j < 4; j++) {
-                const int d = ((t + 8) & 15) - 8;
-                dg[j] |= ((uint32_t)d & 0xFu) << (4 * k);
+            int t = qd.qint[g][8 * w + k];
+            int d = 0;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                d = ((t + 8) & 15) - 8;
+                if (jj == j) break;
                 t = (t - d) >> 4;
             }
+            word |= ((uint32_t)d & 0xFu) << (4 * k);
         }
-        qd.digits[g][w] = make_int4((int)dg[0], (int)dg[1], (int)dg[2], (int)dg[3]);
+        ((int*)&qd.digits[g][w])[j] = (int)word;
     }
     if constexpr (KMF) {
         // B operand words: column c = 2g + p is digit plane p of head g
         // (q_int = d0 + 256 d1, d0 in [-128, 127]); slot s = 4r + j of lane
         // group q for piece pc and half h holds dim
         // 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the unpacked codes put it
-        __syncthreads();
         constexpr int NPC = D / 128;
-        for (int e = tid; e < NPC * 2 * 64; e += blockDim.x) {
+        for (int e = tid; e < NPC * 2 * 64; e += 256) {
             const int pc = e / 128, h = (e / 64) & 1, ln = e & 63;
             const int col = ln & 15, qg4 = ln >> 4, gh = col >> 1, pl = col & 1;
             int wd[4];
@@ -391,8 +409,10 @@ void attn_mfma_kernel(AttnArgs a) {
     }
 
     // query digits of a single head in scalar registers for the whole loop
-    // (uniform operands of v_dot8) when codes are read per key
+    // (uniform operands of v_dot8) when codes are read per key, and the int8
+    // MFMA B operands of the K residual dot (loop invariant)
     int sdig[(G == 1 && RES && !LIN_K) ? CW : 1][4];
+    v4i_t bq[KMF ? NPC : 1][2];
     if constexpr (G == 1 && RES && !LIN_K) {
 #pragma unroll
         for (int w = 0; w < CW; w++) {
@@ -403,9 +423,6 @@ void attn_mfma_kernel(AttnArgs a) {
             sdig[w][3] = __builtin_amdgcn_readfirstlane(dg.w);
         }
     }
-
-    // int8 MFMA B operands of the K residual dot (loop invariant)
-    v4i_t bq[KMF ? NPC : 1][2];
     if constexpr (KMF) {
 #pragma unroll
         for (int pc = 0; pc < NPC; pc++)
@@ -963,6 +980,7 @@ void attn_mfma_kernel(AttnArgs a) {
     // would wait for all of them at the first staging-buffer read), so the
     // prefetch issued before an iteration's second tile lands by its end.
     int t = key_begin + wave * 64;
+
     if constexpr (MODE == MODE_ADAPTIVE) {
         // popcounts and binary scales two tiles ahead, selection and residual
         // gathers one tile ahead; each iteration (two tiles) starts with no
@@ -1047,6 +1065,25 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     }
     if (lane == 0) wsc[wave] = ldexpf(1.0f, -wexp);
+    // per head: the maximum M over the waves, each wave's factor
+    // 2^(m_w - M) * 2^-wexp_w (0 for a wave without keys) and the total l
+    // (published by the first barrier of the head batches below)
+    __shared__ float mfac[4][G], hsum[2][G];
+    __syncthreads();
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        float M = -INFINITY;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+        float lv = 0.0f;
+        for (int w = 0; w < 4; w++) {
+            const bool live = M != -INFINITY && wm[w][g] != -INFINITY;
+            const float f = live ? exp2f(wm[w][g] - M) : 0.0f;
+            mfac[w][g] = f * wsc[w];
+            if (live) lv += f * wlsum[w][g];
+        }
+        hsum[0][g] = M;
+        hsum[1][g] = lv;
+    }
     float* accw = (float*)lds_st0[wave];
     // hi + lo columns are adjacent lanes (col 2g, 2g+1); the even lane writes
     const bool writer = my_col < 2 * G && (my_col & 1) == 0;
@@ -1091,26 +1128,20 @@ void attn_mfma_kernel(AttnArgs a) {
         const int nh = min(HP, G - g0);
         for (int i = threadIdx.x; i < nh * D; i += blockDim.x) {
             const int hs2 = i / D, e = i % D, g = g0 + hs2;
-            float M = -INFINITY;
-            for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
-            float accv = 0.0f, lv = 0.0f;
-            if (M != -INFINITY) {
-                for (int w = 0; w < 4; w++) {
-                    if (wm[w][g] == -INFINITY) continue;
-                    const float f = exp2f(wm[w][g] - M);
-                    const float* aw = (const float*)lds_st0[w];
-                    float v = aw[(0 * HP + hs2) * D + e];
-                    if (RES) v += aw[(1 * HP + hs2) * D + e];
-                    v = (v * two24 - wofs[w][g]) * wsc[w];
-                    accv += f * v;
-                    lv += f * wlsum[w][g];
-                }
+            float accv = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float* aw = (const float*)lds_st0[w];
+                float v = aw[(0 * HP + hs2) * D + e];
+                if (RES) v += aw[(1 * HP + hs2) * D + e];
+                const float f = mfac[w][g];
+                accv += f == 0.0f ? 0.0f : (v * two24 - wofs[w][g]) * f;
             }
             float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
             dst[2 + e] = accv;
             if (e == 0) {
-                dst[0] = M;
-                dst[1] = lv;
+                dst[0] = hsum[0][g];
+                dst[1] = hsum[1][g];
             }
         }
     }
