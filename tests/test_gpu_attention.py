@@ -77,6 +77,43 @@ def test_compensated_and_binary_vs_oracle(F, shape):
     close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
 
 
+# launches with more (b, head group) workgroups than a round of resident
+# workgroups holds (one split each, several rounds), and the split-phase API
+LAUNCH_SHAPES = [
+    (48, 32, 32, 300, 128),    # 1536 MHA groups
+    (64, 32, 8, 520, 128),     # 512 GQA-4 groups, 520 keys
+    (24, 64, 8, 200, 64),      # GQA 8 at d = 64, ragged last tile
+]
+
+
+@pytest.mark.parametrize("shape", LAUNCH_SHAPES, ids=[str(s) for s in LAUNCH_SHAPES])
+def test_many_groups_and_split_phase_api(F, shape):
+    """Full attention calls and the split-phase pair (partials, then combine;
+    a fixed split plan for either mode) against the oracle."""
+    from bitcache_amd import _C
+    B, Hq, Hkv, S, d = shape
+    say(f"case launch {shape}")
+    q, k, v = make(B, Hq, Hkv, S, d, seed=S + B, lognorm=0.25)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    _, refb = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    out = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
+    outb = F.binary_attention(qt, kb, vb, B, Hq, S, d, n_kv_heads=Hkv)
+    close(to_np(out).astype(np.float32), ref, what=f"compensated {shape}")
+    close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
+    ws = _C.attention_partial(qt, kb, kr, vb, vr, B, Hq, Hkv, S, S, d)
+    outp = _C.attention_combine(ws, B, Hq, Hkv, S, d)
+    wsb = _C.attention_partial(qt, kb, None, vb, None, B, Hq, Hkv, S, S, d)
+    outpb = _C.attention_combine(wsb, B, Hq, Hkv, S, d)
+    close(to_np(outp).astype(np.float32), ref, what=f"split-phase compensated {shape}")
+    close(to_np(outpb).astype(np.float32), refb, what=f"split-phase binary {shape}")
+
+
 @pytest.mark.parametrize("H,Hkv,d", [(4, 4, 128), (8, 2, 128), (8, 2, 256)])
 def test_kv_stride_and_zero_length(F, H, Hkv, d):
     say(f"case kv_stride H={H} Hkv={Hkv} d={d}")
