@@ -227,3 +227,33 @@ def test_config_c3_full_size(F):
     say(f"c3 compensated vs exact fp16 attention: mean cos {cos.mean().item():.5f} "
         f"min {cos.min().item():.5f}")
     assert cos.mean().item() > 0.9
+
+
+@pytest.mark.parametrize("group,d", [(2, 128), (4, 128), (8, 128), (4, 64), (4, 256)])
+def test_gqa_equals_mha_on_repeated_kv(F, group, d):
+    """GQA head mapping pinned by its closed form: attention with n_kv_heads =
+    Hq / group equals MHA attention over K/V whose heads are repeated group
+    times (each repeated vector encodes to the same bits).  The two run
+    different kernels (int8-MFMA residual dots over a head group against
+    per-head v_dot8 dots) and split plans; their outputs agree to the output
+    tolerance."""
+    B, Hq, S = 2, 16, 1500
+    Hkv = Hq // group
+    say(f"case gqa==mha group={group} d={d}")
+    q, k, v = make(B, Hq, Hkv, S, d, seed=group * 1000 + d, lognorm=0.25)
+    kr_ = np.repeat(k, group, axis=1)
+    vr_ = np.repeat(v, group, axis=1)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    kbm, krm = encode_gpu(F, kr_)
+    vbm, vrm = encode_gpu(F, vr_)
+    qt = torch.from_numpy(q).cuda()
+    for comp in (True, False):
+        if comp:
+            g = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
+            m = F.compensated_attention(qt, kbm, krm, vbm, vrm, B, Hq, S, d)
+        else:
+            g = F.binary_attention(qt, kb, vb, B, Hq, S, d, n_kv_heads=Hkv)
+            m = F.binary_attention(qt, kbm, vbm, B, Hq, S, d)
+        close(to_np(g).astype(np.float32), to_np(m).astype(np.float32),
+              what=f"gqa vs mha group={group} d={d} comp={comp}")
