@@ -799,12 +799,11 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
 }
 
 // The split policy of a full attention call (plan_splits' per_cu): MHA
-// compensated attention several rounds; binary and GQA compensated attention
-// one round of three workgroups per CU; adaptive attention one round of what
-// fits (its LDS allows two workgroups per CU at d = 128), at most three.
+// compensated attention several rounds; binary, GQA compensated and adaptive
+// attention one round of what fits of their kernel, at most three workgroups
+// per CU (the adaptive kernel's LDS allows two at d = 128).
 int plan_per_cu(int mode, int D, int G) {
     if (mode == MODE_COMP && G == 1) return 0;
-    if (mode != MODE_ADAPTIVE) return 3;
     const int n = bc::mfma_wgs_per_cu(mode, D, G);
     return n <= 0 ? 3 : (n < 3 ? n : 3);
 }
