@@ -662,16 +662,19 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
 // ---------------------------------------------------------------- entropy
 // src/adaptive_precision.cu:196-313.  Tree-order scale_q (thread t of 128
 // holds |q_t| + |q_{t+128}|, tree s = 64..1), scores without 1/sqrt(d),
-// H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread.
+// H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread,
+// merged over the block.  One block of kEntropyThreads per (b, h).
+constexpr int kEntropyThreads = 1024;
 template <int D>
-__global__ __launch_bounds__(256) void entropy_kernel(const uint16_t* q, BinPlanes kb, float* out,
-                                                     int S) {
+__global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t* q, BinPlanes kb,
+                                                                  float* out, int S) {
+    constexpr int NW = kEntropyThreads / 64;
     __shared__ float part[128];
     __shared__ uint32_t qs[D / 32];
-    __shared__ float sm[256], sz[256], sw[256];
+    __shared__ float sm[NW], sz[NW], sw[NW];
     const int bh = blockIdx.x;
     const uint16_t* qb = q + (int64_t)bh * D;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 128) {
         float local = 0.0f;
         for (int i = tid; i < D; i += 128) local += fabsf(h2f(qb[i]));
@@ -689,32 +692,59 @@ __global__ __launch_bounds__(256) void entropy_kernel(const uint16_t* q, BinPlan
     }
     const float sq = part[0] / (float)D;
     const int64_t base = (int64_t)bh * S;
+    // online (M, Z, W) per thread over keys tid, tid + T, ...; four keys'
+    // loads in flight per thread
+    constexpr int U = 4;
     float M = -1e30f, Z = 0.0f, W = 0.0f;
-    for (int s = tid; s < S; s += blockDim.x) {
-        const SignWords<D> ks = load_signs<D>(kb.signs + (base + s) * (D / 8));
-        int pc = 0;
+    for (int s0 = tid; s0 < S; s0 += U * kEntropyThreads) {
+        SignWords<D> ks[U];
+        float skv[U];
 #pragma unroll
-        for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks.w[w]));
-        const float sc = sq * h2f(kb.scales[base + s]) * (float)(2 * pc - D);
-        if (sc > M) {
-            const float f = expf(M - sc);
-            Z *= f;
-            W *= f;
-            M = sc;
+        for (int u = 0; u < U; u++) {
+            const int s = s0 + u * kEntropyThreads;
+            const int64_t i = base + (s < S ? s : s0);
+            ks[u] = load_signs<D, true>(kb.signs + i * (D / 8));
+            skv[u] = h2f(kb.scales[i]);
         }
-        const float e = expf(sc - M);
-        Z += e;
-        W += e * sc;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (s0 + u * kEntropyThreads >= S) break;
+            int pc = 0;
+#pragma unroll
+            for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks[u].w[w]));
+            const float sc = sq * skv[u] * (float)(2 * pc - D);
+            if (sc > M) {
+                const float f = expf(M - sc);
+                Z *= f;
+                W *= f;
+                M = sc;
+            }
+            const float e = expf(sc - M);
+            Z += e;
+            W += e * sc;
+        }
     }
-    sm[tid] = M;
-    sz[tid] = Z;
-    sw[tid] = W;
+    // merge: (M, Z, W) of two key sets is (max, Z1 f1 + Z2 f2, W1 f1 + W2 f2)
+    // with f_i = e^(M_i - max); a butterfly over each wave, then the waves
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float m2 = __shfl_xor(M, off, 64), z2 = __shfl_xor(Z, off, 64), w2 = __shfl_xor(W, off, 64);
+        const float mm = fmaxf(M, m2);
+        const float f1 = expf(M - mm), f2 = expf(m2 - mm);
+        Z = Z * f1 + z2 * f2;
+        W = W * f1 + w2 * f2;
+        M = mm;
+    }
+    if (lane == 0) {
+        sm[wave] = M;
+        sz[wave] = Z;
+        sw[wave] = W;
+    }
     __syncthreads();
     if (tid == 0) {
         float gm = -1e30f;
-        for (int i = 0; i < (int)blockDim.x; i++) gm = fmaxf(gm, sm[i]);
+        for (int i = 0; i < NW; i++) gm = fmaxf(gm, sm[i]);
         float z = 0.0f, w = 0.0f;
-        for (int i = 0; i < (int)blockDim.x; i++) {
+        for (int i = 0; i < NW; i++) {
             const float f = expf(sm[i] - gm);
             z += sz[i] * f;
             w += sw[i] * f;
@@ -1047,7 +1077,7 @@ extern "C" int bc_binary_scores(const void* q, const void* k_bin, float* scores,
 
 template <int D>
 static void launch_entropy(const void* q, BinPlanes kb, float* out, int bh, int S, hipStream_t st) {
-    hipLaunchKernelGGL((entropy_kernel<D>), dim3(bh), dim3(256), 0, st, (const uint16_t*)q, kb,
+    hipLaunchKernelGGL((entropy_kernel<D>), dim3(bh), dim3(kEntropyThreads), 0, st, (const uint16_t*)q, kb,
                        out, S);
 }
 
