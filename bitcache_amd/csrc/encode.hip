@@ -242,9 +242,28 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
                 }
                 const float absmax = m;
                 const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
-                uint32_t word = 0;
+                float y[8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) word |= ((uint32_t)quant7(r[k] * inv) & 0xFu) << (4 * k);
+                for (int k = 0; k < 8; k++) y[k] = r[k] * inv;
+                // a NaN among the scaled residuals makes their sum NaN (otherwise
+                // each is finite and within 7 in magnitude)
+                float t = y[0];
+#pragma unroll
+                for (int k = 1; k < 8; k++) t += y[k];
+                uint32_t word = 0;
+                if (__ballot(!(t == t)) == 0ull) {
+                    // clamp to [-7, 7], then round half to even by adding 1.5 * 2^23
+                    // (unit in the last place 1): the low nibble of the sum's bits
+                    // is the code in two's complement, as quant7 gives it
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        const float c = __builtin_amdgcn_fmed3f(y[k], -7.0f, 7.0f) + 12582912.0f;
+                        word |= (__builtin_bit_cast(uint32_t, c) & 0xFu) << (4 * k);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) word |= ((uint32_t)quant7(y[k]) & 0xFu) << (4 * k);
+                }
                 if (live) {
                     ((uint32_t*)(J.code_plane + dv * (D / 2)))[j] = word;
                     if (j == 0) J.rscale_plane[dv] = f2h(absmax);
