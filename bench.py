@@ -12,8 +12,8 @@ the stream it runs on; cpu_baseline = the CPU oracle (PyTorch-CPU
 restatement) on a bounded sample of the same heads, extrapolated to a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fp16]
-       python bench.py --config c2|c4|c5   (one line for another workload; the
-       headline and the driver's line is the default c3)
+       python bench.py --config c2|c4|c5|prefill   (one line for another
+       workload; the headline and the driver's line is the default c3)
 """
 from __future__ import annotations
 
@@ -38,8 +38,8 @@ def parse():
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 reference kernel")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
-                    help="workload (default c3, the headline)")
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5", "prefill"],
+                    help="workload (default c3, the headline; prefill: the encoders of the c3 cache)")
     ap.add_argument("--probe", action="store_true",
                     help="counter pass for rocprofv3 --pmc: one 1 GiB device copy (calibration) "
                          "then --steps attention steps, no timing output")
@@ -277,6 +277,44 @@ def bench_c5(args, torch, _C, W):
     }
 
 
+def bench_prefill(args, torch, _C, W):
+    """Prefill encode of the c3 cache (rows a2-a4): each of K and V of the c3
+    workload (8 x 32 x 65536 vectors of d = 128, fp16) encoded to sign bits +
+    fp16 scale + INT4 residual + fp16 absmax in one pass (the two-step
+    reference semantics, fp16-rounded scale); and the per-head entropy of the
+    binary scores (row a10) over the encoded K."""
+    cfg = W.CONFIGS["c3"]
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, v = W.make_qkv(cfg)
+    n = B * H * S
+    kf, vf = k.view(-1, d), v.view(-1, d)
+    steps = max(3, min(args.steps, 10))
+    enc_ms = event_ms(lambda: (_C.encode_fused(kf, False), _C.encode_fused(vf, False)), steps, torch) / 2
+    kb, _ = _C.encode_fused(kf, False)
+    del k, v, kf, vf
+    torch.cuda.synchronize()
+    ent_ms = event_ms(lambda: _C.compute_head_entropy(q, kb, B, H, S, d), steps, torch)
+    per_vec = 2 * d + (d // 8 + 2) + (d // 2 + 2)      # fp16 in; signs, scale, codes, absmax out
+    alg = n * per_vec
+    gbs = alg / (enc_ms * 1e-3) / 1e9
+    ent_bytes = n * (d // 8 + 2)
+    return {
+        "metric": "prefill encode µs per K or V tensor + achieved GB/s, c3 cache (16.8M vectors, d=128)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": 0,
+        "ms_per_step": round(enc_ms, 4), "us_per_step": round(enc_ms * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "prefill: encode_fused (sign bits + fp16 scale + INT4 residual) of one "
+                               "c3 K or V tensor; head entropy over the encoded K",
+                   "vectors": n, "head_dim": d, "bytes_per_tensor": alg},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "encode_rows_kernel<128, fused fp16 scale> (VALU-bound)"},
+        "entropy_us": round(ent_ms * 1e3, 1),
+        "entropy_gbps": round(ent_bytes / (ent_ms * 1e-3) / 1e9, 1),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -300,7 +338,8 @@ def main():
     if args.config != "c3":
         fn = {"c2": lambda: bench_c2(args, torch, _C, W),
               "c4": lambda: bench_c4(args, torch, _C, W, bitcache_amd),
-              "c5": lambda: bench_c5(args, torch, _C, W)}[args.config]
+              "c5": lambda: bench_c5(args, torch, _C, W),
+              "prefill": lambda: bench_prefill(args, torch, _C, W)}[args.config]
         print(json.dumps(fn()), flush=True)
         return
 
