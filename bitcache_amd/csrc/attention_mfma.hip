@@ -222,8 +222,20 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
     __syncthreads();
 }
 
-// Resident waves per SIMD the register allocation targets: two for small
-// query groups (memory latency is hidden by the second wave), one otherwise.
+// Build-time switches; each default is the measured fastest on MI355X:
+//   BC_MHA_WAVES   waves/SIMD the MHA compensated kernel's registers target (3)
+//   BC_BIN_WAVES   the same for binary attention of groups up to 2 (5)
+//   BC_ADAPT_WAVES the same for adaptive attention up to d = 128 (2; its LDS
+//                  holds two workgroups per CU at d = 128)
+//   BC_LIN_K / BC_LIN_V  code tiles read as linear KiB runs (1) instead of per key
+//   BC_MHA_PIPE / BC_ADAPT_PIPE / BC_GQA_PIPE  one-tile prefetch with two staging
+//                  buffers for MHA (1), adaptive (1) and GQA compensated (0: one
+//                  buffer keeps a third workgroup per CU) kernels
+//   BC_NT_AUX      cache policy of the loads that cover whole KiB runs (K and V
+//                  sign rows, the linear V code tile, the K code blocks of GQA
+//                  groups, linear K code rows): 2 = nontemporal (8-11% faster;
+//                  lines that several loads share keep the default policy)
+//   BC_NT_SCALES   cache policy of the 2-byte scale loads (0: default)
 #ifndef BC_MHA_WAVES
 #define BC_MHA_WAVES 3
 #endif
@@ -245,10 +257,6 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
 #ifndef BC_BIN_WAVES
 #define BC_BIN_WAVES 5
 #endif
-// cache policy of the loads that cover whole KiB runs (K and V sign rows, the
-// linear V code tile, the K code blocks of GQA groups, linear K code rows):
-// 2 = nontemporal (measured 8-11% faster; lines that several loads share,
-// like the per-key 16-byte pieces of a code row, keep the default policy)
 #ifndef BC_NT_AUX
 #define BC_NT_AUX 2
 #endif
