@@ -133,6 +133,16 @@ __device__ __forceinline__ int slot_of(int k) {
     return 16 * g4 + 8 * mh + ((r & 3) << 1) + (r >> 2);
 }
 
+// Adaptive mode packs the keys of a tile that some head selected into
+// positions 0..n-1 of its residual data.  Position j sits in V staging row
+// res_row(j): rows 16g + 0..7 feed MFMA half 0 and rows 16g + 8..15 half 1, so
+// positions 0..31 are exactly the rows of half 0.  res_pos is the inverse.
+__device__ __forceinline__ int res_row(int j) { return 16 * ((j >> 3) & 3) + 8 * (j >> 5) + (j & 7); }
+__device__ __forceinline__ int res_pos(int row) { return 32 * ((row >> 3) & 1) + 8 * (row >> 4) + (row & 7); }
+__device__ __forceinline__ int mbcnt64(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // Query preparation of one workgroup (256 threads), spread over all threads:
 // the query as floats and its sign words (a wave ballot per 64 elements);
 // scale_q (sequential fp32 order, element 0 first) and the fixed-point step dq
@@ -588,17 +598,24 @@ void attn_mfma_kernel(AttnArgs a) {
         issue_v(buf, t0);
         uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
         const uint64_t selany = __ballot(selmask != 0u);
+        const int nsel = __builtin_popcountll(selany);
         const int tr = t0 - key_begin;
         const bool mine = selmask != 0u;
         const int kk = tr + kown;
+        // compacted positions: key s goes to position mbcnt (selected) or to
+        // n + its rank among the others; key_at = the key at position lane
+        const int mb = mbcnt64(selany);
+        const int key_at = __builtin_amdgcn_ds_permute(4 * (mine ? mb : nsel + lane - mb), lane);
         r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, mine ? kk * 2 : kOob, 0, 0);
         r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, mine ? kk * 2 : kOob, 0, 0);
         if constexpr (KMF) {
-            // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
+            // key block kb: position 16kb + l%16, 16-byte piece l/16 + 4pc of
+            // its key's row
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
-                const bool sel_k = (selany >> (16 * kb + lj)) & 1ull;
-                const int base = sel_k ? (tr + 16 * kb + lj) * CB + 16 * g4 : kOob;
+                const int j = 16 * kb + lj;
+                const int key = __builtin_amdgcn_ds_bpermute(4 * j, key_at);
+                const int base = j < nsel ? (tr + key) * CB + 16 * g4 : kOob;
 #pragma unroll
                 for (int pc = 0; pc < NPC; pc++) {
                     const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 64 * pc, 0, 0);
@@ -613,10 +630,13 @@ void attn_mfma_kernel(AttnArgs a) {
                 r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
             }
         }
+        // V codes: staging row lane holds position res_pos(lane)
+        const int jv = res_pos(lane);
+        const int vkey = __builtin_amdgcn_ds_bpermute(4 * jv, key_at);
 #pragma unroll
         for (int c = 0; c < Q; c++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
-                                                     mine ? kk * CB + 16 * c : kOob, 0, 0, 0);
+                                                     jv < nsel ? (tr + vkey) * CB + 16 * c : kOob, 0, 0, 0);
     };
 
     // ---------------- one tile: scores, online softmax, value MFMAs
@@ -660,7 +680,16 @@ void attn_mfma_kernel(AttnArgs a) {
             const float mq = (float)(2 * pc - D);
             xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:179)
         }
-        if constexpr (MODE == MODE_ADAPTIVE) selmask = r.sel;
+        // adaptive: the tile's compacted residual positions (as in gather):
+        // nsel selected keys, the lane's key at position rpos
+        int nsel = 64, rpos = kown;
+        if constexpr (MODE == MODE_ADAPTIVE) {
+            selmask = r.sel;
+            const uint64_t selany = __ballot(selmask != 0u);
+            const int mb = mbcnt64(selany);
+            nsel = __builtin_popcountll(selany);
+            rpos = selmask != 0u ? mb : nsel + lane - mb;
+        }
         if constexpr (MODE == MODE_ADAPTIVE) {
             if (a.selected != nullptr && valid) {
 #pragma unroll
@@ -674,9 +703,10 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) racc[g] = 0;
         if constexpr (KMF) {
-          bool kmf_run = true;
-          if constexpr (MODE == MODE_ADAPTIVE) kmf_run = __ballot(selmask != 0u) != 0ull;
-          if (kmf_run) {
+          // key blocks holding codes: all four, or (adaptive) the blocks of
+          // the nsel compacted positions
+          const int nkb = (nsel + 15) >> 4;
+          if (nkb > 0) {
             // codes as int8 16*n (signed): low nibbles via x << 4, high nibbles in
             // place; each half of a piece is one 16x16x64 MFMA of (head, digit
             // plane) rows x 64 dims times 64 dims x 16 keys (columns of keys whose
@@ -684,6 +714,7 @@ void attn_mfma_kernel(AttnArgs a) {
             v4i_t acc[4];
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
+                if (kb >= nkb) break;
                 acc[kb] = v4i_t{0, 0, 0, 0};
 #pragma unroll
                 for (int pc = 0; pc < NPC; pc++)
@@ -697,27 +728,30 @@ void attn_mfma_kernel(AttnArgs a) {
                     }
             }
             // lane l holds rows 4(l/16) + i = (head 2(l/16) + i/2, plane i%2) of
-            // key 16kb + l%16: both planes of a head sit in one lane, and
-            // q_int dot * 16 = plane0 + 256 plane1 goes to rdl[key][head]
+            // position 16kb + l%16: both planes of a head sit in one lane, and
+            // q_int dot * 16 = plane0 + 256 plane1 goes to rdl[position][head]
             if (lane < 8 * G) {
 #pragma unroll
-                for (int kb = 0; kb < 4; kb++)
+                for (int kb = 0; kb < 4; kb++) {
+                    if (kb >= nkb) break;
                     *(int2*)&rdl[(16 * kb + lj) * G + 2 * g4] =
                         make_int2(acc[kb][0] + 256 * acc[kb][1], acc[kb][2] + 256 * acc[kb][3]);
+                }
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             // kept x16: the factor is folded into the score's scale below
+            // (lanes past the written positions read values they never use)
             if constexpr (G % 4 == 0) {
 #pragma unroll
                 for (int g = 0; g < G; g += 4) {
-                    const int4 v = *(const int4*)&rdl[lane * G + g];
+                    const int4 v = *(const int4*)&rdl[rpos * G + g];
                     racc[g] = v.x; racc[g + 1] = v.y; racc[g + 2] = v.z; racc[g + 3] = v.w;
                 }
             } else {
 #pragma unroll
-                for (int g = 0; g < G; g++) racc[g] = rdl[lane * G + g];
+                for (int g = 0; g < G; g++) racc[g] = rdl[rpos * G + g];
             }
           }
         } else if constexpr (LIN_K) {
@@ -826,15 +860,24 @@ void attn_mfma_kernel(AttnArgs a) {
         // online softmax; (hi, lo) fp16 weights to LDS in MFMA slot order
         float lane_alpha = 1.0f;
         bool any_rescale = false;
-        // the value operands of odd keys come out 16x larger (see the MFMA
+        // the value operands of odd rows come out 16x larger (see the MFMA
         // loops below): their weights carry 1/16 so that every product is exact
+        // (the residual row of a key is its compacted position's row, of the
+        // parity of rpos)
         const float kfac = (kown & 1) ? 0.0625f : 1.0f;
+        const float kfac_res = (rpos & 1) ? 0.0625f : 1.0f;
         // per-key factors shared by the heads: sign weight a2 = p * fa, residual
         // weight b = p * fb, and the offset sum_s (a_s + 8 b_s) grows by p * fo
         const float fa = ldexpf(2.0f * svv * kfac, wexp);
-        const float fb = RES ? ldexpf(rsv * (1.0f / 7.0f) * kfac, wexp) : 0.0f;
+        const float fb = RES ? ldexpf(rsv * (1.0f / 7.0f) * kfac_res, wexp) : 0.0f;
         const float fo_bin = ldexpf(svv, wexp);
         const float fo_res = RES ? ldexpf(svv + rsv * (8.0f / 7.0f), wexp) : fo_bin;
+        // residual weights go to the slot of the key's residual position
+        // (adaptive: compacted; unselected keys write zeros to the positions
+        // past nsel, so every slot a residual MFMA reads is written)
+        uint16_t* wres = wsl;
+        if constexpr (MODE == MODE_ADAPTIVE)
+            wres = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + slot_of(res_row(rpos)));
 #pragma unroll
         for (int g = 0; g < G; g++) {
             // the reference m[g] moves only when a score passes m[g] + kTau
@@ -871,8 +914,8 @@ void attn_mfma_kernel(AttnArgs a) {
             wsl[(0 * 2 * G + 2 * g) * WL::kColSlots] = a2h;
             wsl[(0 * 2 * G + 2 * g + 1) * WL::kColSlots] = a2l;
             if constexpr (RES) {
-                wsl[(1 * 2 * G + 2 * g) * WL::kColSlots] = bh;
-                wsl[(1 * 2 * G + 2 * g + 1) * WL::kColSlots] = bl;
+                wres[(1 * 2 * G + 2 * g) * WL::kColSlots] = bh;
+                wres[(1 * 2 * G + 2 * g + 1) * WL::kColSlots] = bl;
             }
         }
         if (any_rescale) {
@@ -912,15 +955,15 @@ void attn_mfma_kernel(AttnArgs a) {
         // all transposed reads of the tile first (they retire in order while
         // the MFMAs of earlier blocks run)
         const int row_key = 16 * g4 + lj;  // this lane addresses row (key) lj of its group
-        bool any_sel = true;
-        if constexpr (MODE == MODE_ADAPTIVE) any_sel = __ballot(selmask != 0u) != 0ull;
+        // MFMA halves that hold residual positions (adaptive: ceil(nsel / 32))
+        const int nmh = (nsel + 31) >> 5;
         v2i_t wsg[NH];
 #pragma unroll
         for (int h = 0; h < NH; h++)
             wsg[h] = __builtin_amdgcn_ds_read_tr4_b64_v2i32(LDS_PTR(v2i_t, st_signs + SB * row_key + 8 * h));
         v2i_t wrs[RES ? NB : 1];
         if constexpr (RES) {
-            if (any_sel) {
+            if (nmh > 0) {
 #pragma unroll
                 for (int db = 0; db < NB; db++) {
                     const uint8_t* rp = LIN_V ? st_codes + CB * row_key + 16 * ((db >> 1) ^ vsw) + 8 * (db & 1)
@@ -954,24 +997,31 @@ void attn_mfma_kernel(AttnArgs a) {
         }
 
         // residual part: rows = dims 16db + lj
-        if constexpr (RES) {
-            if (any_sel) {
+        auto res_mfma = [&](int db, int mh) {
+            // u = n + 8 in place: keys k, k + 4 at 4(k&1) (odd keys 16x)
+            const uint32_t x = (uint32_t)(mh ? wrs[db].y : wrs[db].x) ^ 0x88888888u;
+            const uint32_t y = x >> 8;
+            uint32_t pw[4];
+            pw[0] = x & 0x000F000Fu;
+            pw[1] = x & 0x00F000F0u;
+            pw[2] = y & 0x000F000Fu;
+            pw[3] = y & 0x00F000F0u;
+            const h8_t av = __builtin_bit_cast(h8_t, pw);
+            cn[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bres[mh], cn[db], 0, 0, 0);
+        };
+        if constexpr (MODE == MODE_ADAPTIVE) {
+            // half 0 when any key is selected, half 1 only past 32 of them
 #pragma unroll
-                for (int db = 0; db < NB; db++) {
+            for (int mh = 0; mh < 2; mh++) {
+                if (mh >= nmh) break;
 #pragma unroll
-                    for (int mh = 0; mh < 2; mh++) {
-                        // u = n + 8 in place: keys k, k + 4 at 4(k&1) (odd keys 16x)
-                        const uint32_t x = (uint32_t)(mh ? wrs[db].y : wrs[db].x) ^ 0x88888888u;
-                        const uint32_t y = x >> 8;
-                        uint32_t pw[4];
-                        pw[0] = x & 0x000F000Fu;
-                        pw[1] = x & 0x00F000F0u;
-                        pw[2] = y & 0x000F000Fu;
-                        pw[3] = y & 0x00F000F0u;
-                        const h8_t av = __builtin_bit_cast(h8_t, pw);
-                        cn[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bres[mh], cn[db], 0, 0, 0);
-                    }
-                }
+                for (int db = 0; db < NB; db++) res_mfma(db, mh);
+            }
+        } else if constexpr (RES) {
+#pragma unroll
+            for (int db = 0; db < NB; db++) {
+                res_mfma(db, 0);
+                res_mfma(db, 1);
             }
         }
         // the staging buffer is refilled two tiles later: its reads retire here
