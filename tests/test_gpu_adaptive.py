@@ -114,6 +114,59 @@ def test_config_c5_sample(F):
     close(to_np(out).astype(np.float32), ref, what="c5 sample")
 
 
+def test_config_c5_full_size(F):
+    """Config c5 at full size (B16, GQA 32/8, S = 131072, top 10%).  Every one of
+    the 512 selected sets is checked against the definition of the top-k, a
+    property that does not depend on S: exactly k keys; no unselected key ranks
+    above a selected one; keys equal to the threshold are taken lowest index
+    first.  The ranking key scale_k * (2pc - d) comes from the GPU independently
+    of the kernels under test: 2pc - d = sign(k) . sign(q) is an exact +-1
+    matmul in fp32 and the product with the fp16 scale is exact.  Two head
+    groups are also compared with the oracle (sets and outputs)."""
+    from bitcache_amd import workloads as W
+    say("case c5 full size")
+    cfg = W.CONFIGS["c5"]
+    B, Hq, Hkv, S, d = cfg.batch, cfg.n_heads, cfg.n_kv_heads, cfg.seq_len, cfg.head_dim
+    G = Hq // Hkv
+    q, k, v = W.make_qkv(cfg)
+    kb, kr = F.encode_fused(k.view(-1, d))
+    vb, vr = F.encode_fused(v.view(-1, d))
+    top_k = O.default_top_k(S)
+    out, sel = F.adaptive_attention(q, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv, top_k=top_k,
+                                    return_selected=True)
+    torch.cuda.synchronize()
+    n = B * Hkv * S
+    kscale = kb[n * d // 8:n * d // 8 + 2 * n].view(torch.float16).view(B, Hkv, S).float()
+    idx = torch.arange(S, device=q.device)
+    for b in range(B):
+        sk = torch.where(k[b] >= 0, 1.0, -1.0)                                  # [Hkv, S, d]
+        sq = torch.where(q[b] >= 0, 1.0, -1.0).view(Hkv, G, d).transpose(1, 2).contiguous()
+        dots = torch.bmm(sk, sq)                                                # [Hkv, S, G]
+        key = (kscale[b][..., None] * dots).permute(0, 2, 1).reshape(Hq, S)     # exact in fp32
+        s = sel[b].bool()
+        assert torch.equal(s.sum(-1), torch.full((Hq,), top_k, device=q.device)), f"set sizes, b={b}"
+        lo_sel = torch.where(s, key, torch.inf).amin(-1)
+        hi_uns = torch.where(~s, key, -torch.inf).amax(-1)
+        assert bool((lo_sel >= hi_uns).all()), f"an unselected key ranks above a selected one, b={b}"
+        tie = lo_sel == hi_uns
+        last_sel = torch.where(s & (key == lo_sel[:, None]), idx, -1).amax(-1)
+        first_uns = torch.where(~s & (key == lo_sel[:, None]), idx, S).amin(-1)
+        assert bool((last_sel < first_uns)[tie].all()), f"ties not taken lowest index first, b={b}"
+    for b, kvh in [(0, 0), (15, 7)]:
+        Kb, Kr = O.encode_fused(to_np(k[b, kvh]))
+        Vb, Vr = O.encode_fused(to_np(v[b, kvh]))
+        qg = to_np(q[b, kvh * G:(kvh + 1) * G])[None]
+        _, ref, sets = O.adaptive_attention(qg, Kb, Kr, Vb, Vr, 1, G, S, top_k, n_kv_heads=1,
+                                            return_f32=True, return_sets=True)
+        for (_, h), want in sets.items():
+            got = np.nonzero(to_np(sel[b, kvh * G + h]))[0]
+            assert np.array_equal(got, want), f"set differs at (b={b}, h={kvh * G + h})"
+        close(to_np(out[b, kvh * G:(kvh + 1) * G]).astype(np.float32), ref[0],
+              what=f"c5 full size group {(b, kvh)}")
+    del q, k, v, kb, kr, vb, vr, out, sel
+    torch.cuda.empty_cache()
+
+
 def test_adaptive_special_scales(F):
     """Selected sets with planted K scales: +-inf, NaN, +-0, negative, the
     fp16 maximum and a subnormal.  Waves holding a non-finite scale rank by the

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.gpu_util import close, say, to_np
+from tests.gpu_util import close, say, slice_enc, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -92,3 +92,50 @@ def test_bitcache_rejects_bad_inputs():
     with pytest.raises(AssertionError):
         c.append(torch.zeros((1, 2, 128), dtype=torch.float32, device="cuda"),
                  torch.zeros((1, 2, 128), dtype=torch.float32, device="cuda"))
+
+
+def test_config_c4_full_size():
+    """Config c4 at full size (B4, GQA 32/8, 16384-token prefill + 256 decode
+    steps of append + attend, as bench.py runs it).  Size-independent checks:
+    the cache after the loop is bit-identical to a one-shot prefill of all
+    16640 tokens (appends == prefill), and the outputs of the first, middle and
+    last steps for two head groups match the oracle (online encode of the
+    group's tokens, then compensated attention over them)."""
+    from bitcache_amd import BitCache
+    from bitcache_amd import workloads as W
+    say("case c4 full size")
+    cfg = W.CONFIGS["c4"]
+    B, Hq, Hkv, S, d = cfg.batch, cfg.n_heads, cfg.n_kv_heads, cfg.seq_len, cfg.head_dim
+    G, T = Hq // Hkv, W.C4_DECODE_STEPS
+    _, k, v = W.make_qkv(cfg)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(cfg.seed + 100)
+    qs = (torch.randn((T, B, Hq, d), generator=g, device="cuda") * W.SIGMA).half()
+    ks = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
+    vs = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
+    cache = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
+    cache.prefill(k, v)
+    outs = {}
+    for t in range(T):
+        cache.append(ks[t], vs[t])
+        o = cache.attend(qs[t])
+        if t in (0, T // 2, T - 1):
+            outs[t] = o.clone()
+    assert cache.seq_len == S + T
+    kall = torch.cat([k, ks.permute(1, 2, 0, 3)], dim=2).contiguous()
+    vall = torch.cat([v, vs.permute(1, 2, 0, 3)], dim=2).contiguous()
+    once = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
+    once.prefill(kall, vall)
+    for x, y in ((cache._k_bin, once._k_bin), (cache._v_bin, once._v_bin),
+                 (cache._k_res, once._k_res), (cache._v_res, once._v_res)):
+        assert torch.equal(x, y)
+    for b, kvh in [(0, 0), (3, 7)]:
+        Kb, Kr = O.online_encode(to_np(kall[b, kvh]))
+        Vb, Vr = O.online_encode(to_np(vall[b, kvh]))
+        for t, o in outs.items():
+            n = S + t + 1
+            enc = [slice_enc(e, 0, n) for e in (Kb, Kr, Vb, Vr)]
+            qg = to_np(qs[t, b, kvh * G:(kvh + 1) * G])[None]
+            ref = O.compensated_attention(qg, *enc, 1, G, n, n_kv_heads=1, return_f32=True)[1]
+            close(to_np(o[b, kvh * G:(kvh + 1) * G]).astype(np.float32), ref[0],
+                  what=f"c4 step {t} group {(b, kvh)}")
