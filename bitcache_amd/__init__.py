@@ -124,6 +124,22 @@ class BitCache:
                             self.batch, self.n_heads, self.n_kv_heads, self._filled,
                             self.max_seq, self.head_dim)
 
+    def append_attend(self, K: Tensor, V: Tensor, Q: Tensor) -> Tensor:
+        """One decode step: append(K, V) followed by attend(Q), with the same
+        cache bytes and output, in one attention launch where the kernels allow
+        it (the append of bitcache/__init__.py:95-113 and the attention of
+        :115-148 fused)."""
+        self._validate_kv(K, V)
+        # tokens appended so far, as the kernels' ring rule reads it: slot =
+        # current % max_seq, attended positions = min(current + 1, max_seq)
+        current = self._write_pos if self._filled < self.max_seq else self._write_pos + self.max_seq
+        out = _C.append_attention(Q, K, V, self._k_bin, self._k_res, self._v_bin, self._v_res,
+                                  self.batch, self.n_heads, self.n_kv_heads, self.head_dim,
+                                  current, self.max_seq)
+        self._write_pos = (self._write_pos + 1) % self.max_seq
+        self._filled = min(self._filled + 1, self.max_seq)
+        return out
+
     def attend_adaptive(self, Q: Tensor, frac: float = 0.10, top_k: Optional[int] = None,
                         return_selected: bool = False):
         """Residual correction only on the top-k keys by binary score per

@@ -24,15 +24,6 @@
 //            | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G] | attention partials.
 #include "attn.h"
 
-namespace bc {
-int run_attention(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
-                  const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
-                  int seq_len, int kv_stride, int head_dim, void* workspace,
-                  size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* cutoff, uint8_t* selected, const void* pcs);
-size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
-}  // namespace bc
-
 namespace {
 using bc::PcPack;
 using bc::PcT;

@@ -842,6 +842,15 @@ int plan_per_cu(int mode, int D, int G) {
 // reference kernel
 constexpr int kPlanFixed = 0;
 
+// BITCACHE_VALU_ATTENTION=1 selects the VALU split kernel for every head dim
+bool valu_forced() {
+    static const bool forced = [] {
+        const char* e = getenv("BITCACHE_VALU_ATTENTION");
+        return e != nullptr && e[0] == '1';
+    }();
+    return forced;
+}
+
 // workspace of the split partials: the largest plan of any mode
 size_t ws_bytes(int batch, int hq, int hkv, int S, int D) {
     int n = 1;
@@ -913,7 +922,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
                 const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
                 hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
-                uint8_t* selected, const void* pcs, int per_cu) {
+                uint8_t* selected, const void* pcs, int per_cu, const AppendArgs* app = nullptr) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -943,15 +952,18 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.cutoff = cutoff;
     a.selected = selected;
     a.pcs = pcs;
+    if (app != nullptr) {
+        a.app_k = (const uint16_t*)app->k;
+        a.app_v = (const uint16_t*)app->v;
+        a.app_slot = app->slot;
+    }
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     // matrix-core value phase for head_dim 64/128/256; the VALU kernel covers the
     // other head dims (and is selectable with BITCACHE_VALU_ATTENTION=1)
-    static const bool force_valu = [] {
-        const char* e = getenv("BITCACHE_VALU_ATTENTION");
-        return e != nullptr && e[0] == '1';
-    }();
-    if (!force_valu && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st))
+    if (!valu_forced() && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st))
         return bc::check_launch("attention split (mfma)");
+    // (the VALU kernel does not append; the append entry point checks first)
+    BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }
@@ -972,12 +984,12 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* cutoff, uint8_t* selected, const void* pcs) {
+                  const int32_t* cutoff, uint8_t* selected, const void* pcs, const AppendArgs* app) {
     const int per_cu = head_dim > 0 && n_kv_heads > 0
                            ? plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads)) : kPlanFixed;
     int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
                          kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
-                         selected, pcs, per_cu);
+                         selected, pcs, per_cu, app);
     if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
@@ -1045,6 +1057,51 @@ extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_
     return bc::run_attention(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, out,
                              batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
                              workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+// One decode step on a ring cache: the new token's K and V vectors go to
+// position current_len % max_seq of every (b, kv head) row (the slot rule of
+// src/online_encode.cu:139, bitcache/__init__.py:112-113), then the query
+// attends over the min(current_len + 1, max_seq) filled positions.  The same
+// bytes and outputs as bc_online_encode_kv followed by bc_attention_gqa; in one
+// launch when the MFMA kernel runs with one query-head group per kv head (the
+// workgroup whose keys hold the slot encodes the token before reading them),
+// otherwise as those two calls.
+extern "C" int bc_append_attention(const void* q, const void* k_new, const void* v_new, void* k_bin,
+                                   void* k_res, void* v_bin, void* v_res, void* out, int batch,
+                                   int n_heads, int n_kv_heads, int head_dim, int64_t current_len,
+                                   int max_seq, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    BC_REQUIRE((k_res == nullptr) == (v_res == nullptr), BC_ERR_INVALID_ARGUMENT,
+               "k_res and v_res must both be given or both be null");
+    BC_REQUIRE(max_seq > 0 && current_len >= 0, BC_ERR_INVALID_ARGUMENT,
+               "invalid ring: max_seq=%d current_len=%lld", max_seq, (long long)current_len);
+    int v = validate_heads(batch, n_heads, n_kv_heads, max_seq, max_seq, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_new && v_new && k_bin && v_bin && out, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const int seq_len = current_len + 1 < max_seq ? (int)(current_len + 1) : max_seq;
+    // (checked before the token is written, so a failed step leaves the cache as it was)
+    const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
+               "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
+    const int mode = k_res ? MODE_COMP : MODE_BINARY;
+    const int group = n_heads / n_kv_heads;
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len,
+                                    plan_per_cu(mode, head_dim, pick_g(group)));
+    hipStream_t st = (hipStream_t)stream;
+    if (valu_forced() || pick_g(group) != group || !bc::mfma_split_ok(head_dim, p.chunk)) {
+        const int rc = bc_online_encode_kv(k_new, v_new, k_bin, k_res, v_bin, v_res, batch,
+                                           n_kv_heads, head_dim, current_len, max_seq, stream);
+        if (rc != BC_OK) return rc;
+        return bc::run_attention(mode, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
+                                 seq_len, max_seq, head_dim, workspace, workspace_bytes, st, nullptr,
+                                 nullptr, nullptr, nullptr);
+    }
+    const bc::AppendArgs app{k_new, v_new, (int)(current_len % max_seq)};
+    return bc::run_attention(mode, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
+                             seq_len, max_seq, head_dim, workspace, workspace_bytes, st, nullptr,
+                             nullptr, nullptr, nullptr, &app);
 }
 
 template <int D>

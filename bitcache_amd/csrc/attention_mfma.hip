@@ -23,6 +23,7 @@
 #include <math.h>
 
 #include "attn.h"
+#include "encode_row.h"
 
 #include <map>
 #include <mutex>
@@ -368,6 +369,33 @@ void attn_mfma_kernel(AttnArgs a) {
     // the copy permutes the pieces within each row (same cache lines).  A
     // lane's transposed reads cover row = lane.
     const int vsw = ((lane * CB) >> 8) & (Q - 1);
+
+    // In-place append: the workgroup whose key range holds the new token's slot
+    // encodes the token's K and V vectors into the cache first (wave 0, lane
+    // groups 0 and 1, online-encode semantics: the residual against the fp32
+    // mean).  Its stores complete before the barrier, so its own tile loads see
+    // them; no other workgroup reads the slot's cache lines (key ranges are
+    // whole 64-key tiles, and the host appends only with one query-head group
+    // per kv head), and later launches see them as after a separate encode.
+    if constexpr (MODE != MODE_ADAPTIVE) {
+        if (a.app_k != nullptr && a.app_slot >= key_begin && a.app_slot < key_end) {
+            if (wave == 0) {
+                constexpr int L = D / 8;
+                const int grp = lane / L, j = lane % L;
+                const bool is_v = grp == 1;
+                const uint16_t* src = (is_v ? a.app_v : a.app_k) + (int64_t)bkv * D;
+                const BinPlanes& bp = is_v ? a.vb : a.kb;
+                const ResPlanes& rp = is_v ? a.vr : a.kr;
+                // (the attention arguments hold the cache planes read-only)
+                const bc::EncodeDst dst{(uint8_t*)bp.signs, (uint16_t*)bp.scales,
+                                        RES ? (uint8_t*)rp.codes : nullptr, RES ? (uint16_t*)rp.scales : nullptr};
+                bc::encode_row<D, RES ? bc::ENC_FUSED_FP32 : bc::ENC_BINARY>(src, j, grp < 2, dst,
+                                                                            kv_base + a.app_slot);
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+            __syncthreads();
+        }
+    }
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
@@ -1272,10 +1300,15 @@ int mfma_wgs_per_cu(int mode, int D, int G) {
     return n;
 }
 
-bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
+bool mfma_split_ok(int D, int64_t chunk) {
+    if (D != 64 && D != 128 && D != 256) return false;
     // buffer offsets are 32-bit and relative to a split's key range; the
     // prefetches reach up to 12 tiles (768 keys) past its end
-    if (((int64_t)a.chunk + 1024) * (D / 2) + 4096 >= ((int64_t)1 << 31)) return false;
+    return (chunk + 1024) * (D / 2) + 4096 < ((int64_t)1 << 31);
+}
+
+bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
+    if (!mfma_split_ok(D, a.chunk)) return false;
     // adaptive mode reads the popcounts stored by the selection passes
     if (mode == MODE_ADAPTIVE && a.pcs == nullptr) return false;
     switch (D) {

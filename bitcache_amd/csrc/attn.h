@@ -25,6 +25,13 @@ struct AttnArgs {
     const void* pcs;             // adaptive: [B*Hq/G][pcs_stride(S)] PcPack<PcT<D>, G>
                                  // popcounts of the selection passes (G = the kernel's
                                  // head group)
+    // in-place append (binary and compensated modes, one query-head group per
+    // kv head): the new K and V vectors [B*Hkv, D] fp16 are encoded into cache
+    // position app_slot of every (b, kv head) row before the row is attended
+    // (null: no append)
+    const uint16_t* app_k;
+    const uint16_t* app_v;
+    int app_slot;
 };
 
 // Packs per row of the stored popcounts: S rounded up to 16, so that every
@@ -44,7 +51,29 @@ struct __attribute__((aligned(G * sizeof(P)))) PcPack {
 // MFMA value-phase kernels (attention_mfma.hip): true if (D, G, mode) is
 // handled there and the launch was issued.
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st);
+// True if the MFMA kernels handle head_dim D with splits of `chunk` keys.
+bool mfma_split_ok(int D, int64_t chunk);
 // Resident workgroups per CU of the MFMA kernel of (mode, D, G) on the current
 // device (0 when no MFMA kernel handles it).
 int mfma_wgs_per_cu(int mode, int D, int G);
+
+// New K/V token encoded into cache position `slot` by the attention launch
+// itself (see AttnArgs::app_k).
+struct AppendArgs {
+    const void* k;   // [B*Hkv, D] fp16
+    const void* v;
+    int slot;
+};
+
+// Split partials + combine (attention.hip), shared by the public entry points
+// and the adaptive driver (adaptive.hip).  app: append the token first (the
+// caller has checked that the MFMA kernel runs with one query-head group per
+// kv head).
+int run_attention(int mode, const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                  const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
+                  int seq_len, int kv_stride, int head_dim, void* workspace,
+                  size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
+                  const int32_t* cutoff, uint8_t* selected, const void* pcs,
+                  const AppendArgs* app = nullptr);
+size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
 }  // namespace bc

@@ -11,15 +11,16 @@
 #include <math.h>
 
 #include "common.h"
+#include "encode_row.h"
 
 namespace {
-
-enum EncodeMode : int {
-    ENC_BINARY = 0,         // bits + scale
-    ENC_FUSED_FP16 = 1,     // bits + scale + residual against the fp16 scale (two-step semantics)
-    ENC_FUSED_FP32 = 2,     // bits + scale + residual against the fp32 mean (online semantics)
-    ENC_RESIDUAL_ONLY = 3,  // residual against bits + fp16 scale read from a binary blob
-};
+using bc::ENC_BINARY;
+using bc::ENC_FUSED_FP16;
+using bc::ENC_FUSED_FP32;
+using bc::ENC_RESIDUAL_ONLY;
+using bc::EncodeDst;
+using bc::encode_row;
+using bc::quant7;
 
 struct EncodeJob {
     const uint16_t* src;          // [n, D] fp16
@@ -31,13 +32,6 @@ struct EncodeJob {
     // destination vector index = (v / row_len) * row_stride + row_offset + v % row_len
     int64_t row_len, row_stride, row_offset;
 };
-
-// __float2int_rn followed by the [-7, 7] clamp of src/residual.cu:237-242; NaN -> 0.
-__device__ __forceinline__ int quant7(float v) {
-    if (!(v == v)) return 0;
-    float c = fminf(fmaxf(v, -7.0f), 7.0f);
-    return (int)__builtin_rintf(c);
-}
 
 template <int D, int MODE>
 __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1) {
@@ -142,19 +136,13 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
 // Row-parallel encoder for d in {64, 128, 256}: L = d/8 lanes per vector, each
 // lane holding 8 consecutive elements (one 16-byte load), so a wave encodes
 // 64/L vectors at once with coalesced loads and stores and all reductions on
-// DPP / swizzle lane moves.  Same arithmetic as encode_kernel: the scale sum
-// follows the reference tree exactly -- element t = 8j + k sits in lane j, so
-// the tree levels s = 64..8 pair lane j with lane j + s/8 (row_shl) and the
-// levels s = 4, 2, 1 are in-lane; d = 256 first adds |x_{t+128}| from the
-// lane 16 above (the reference's per-thread loop), d = 64 skips the s = 64
-// level (it adds +0.0).
+// DPP / swizzle lane moves (encode_row in encode_row.h).  Same arithmetic as
+// encode_kernel.
 template <int D, int MODE>
 __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
     constexpr int L = D / 8;        // lanes per vector
     constexpr int VPW = 64 / L;     // vectors per wave
-    // swizzle pattern that broadcasts lane 0 of each L-lane group (and-mask mode)
-    constexpr int BCAST = L == 8 ? 0x18 : (L == 16 ? 0x10 : 0x00);
     const int lane = threadIdx.x & 63;
     const int sub = lane / L, j = lane % L;
     const int64_t wave_id = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -168,107 +156,8 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
             const int64_t v = live ? v0 : J.n - 1;
             const int64_t dv = J.row_len == 1 ? v * J.row_stride + J.row_offset
                                               : (v / J.row_len) * J.row_stride + J.row_offset + v % J.row_len;
-            // nontemporal: the wave's vectors are one contiguous run read once
-            const bc_v4u raw = __builtin_nontemporal_load((const bc_v4u*)(J.src + v * D) + j);
-            const uint32_t hw[4] = {raw[0], raw[1], raw[2], raw[3]};
-            float x[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) x[k] = h2f((uint16_t)(hw[k >> 1] >> (16 * (k & 1))));
-
-            uint32_t byte = 0;
-            float s;
-            float mean = 0.0f;
-            if constexpr (MODE == ENC_RESIDUAL_ONLY) {
-                byte = J.sign_plane[dv * (D / 8) + j];
-                s = h2f(J.scale_plane[dv]);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; k++) byte |= (x[k] >= 0.0f ? 1u : 0u) << k;  // +-0 -> 1, NaN -> 0
-                float p[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]);
-                if constexpr (D == 256) {
-#pragma unroll
-                    for (int k = 0; k < 8; k++) p[k] = p[k] + swz_f<0x401F>(p[k]);  // + |x_{t+128}|
-                }
-                if constexpr (D >= 128) {
-#pragma unroll
-                    for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x108>(p[k]);   // s = 64
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);       // s = 32
-#pragma unroll
-                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x102>(p[k]);       // s = 16
-#pragma unroll
-                for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x101>(p[k]);       // s = 8
-#pragma unroll
-                for (int k = 0; k < 4; k++) p[k] = p[k] + p[k + 4];                  // s = 4
-                p[0] = p[0] + p[2];
-                p[1] = p[1] + p[3];                                                   // s = 2
-                p[0] = p[0] + p[1];                                                   // s = 1
-                const float total_abs = swz_f<BCAST>(p[0]);
-                mean = total_abs / (float)D;
-                if constexpr (MODE == ENC_FUSED_FP16) s = h2f(f2h(mean));
-                else s = mean;
-                // sign bytes of 4 lanes -> one little-endian word
-                const uint32_t w = byte | (dpp_u<0x101>(byte) << 8) | (dpp_u<0x102>(byte) << 16) |
-                                   (dpp_u<0x103>(byte) << 24);
-                if (live) {
-                    if ((j & 3) == 0) ((uint32_t*)(J.sign_plane + dv * (D / 8)))[j >> 2] = w;
-                    if (j == 0) J.scale_plane[dv] = f2h(mean);
-                }
-            }
-
-            if constexpr (MODE != ENC_BINARY) {
-                if (J.code_plane == nullptr) continue;
-                float r[8];
-                float m = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    r[k] = x[k] - (((byte >> k) & 1u) ? s : -s);
-                    m = fmaxf(m, fabsf(r[k]));
-                }
-                // fmaxf ignores NaN and is order independent (src/residual.cu:201-223)
-                if constexpr (L == 8) {
-                    m = fmaxf(m, dpp_f<0x141>(m));   // half mirror
-                    m = fmaxf(m, dpp_f<0x4E>(m));    // quad 2,3,0,1
-                    m = fmaxf(m, dpp_f<0xB1>(m));    // quad 1,0,3,2
-                } else {
-                    m = fmaxf(m, dpp_f<0x128>(m));   // row rotations
-                    m = fmaxf(m, dpp_f<0x124>(m));
-                    m = fmaxf(m, dpp_f<0x122>(m));
-                    m = fmaxf(m, dpp_f<0x121>(m));
-                    if constexpr (L == 32) m = fmaxf(m, swz_f<0x401F>(m));
-                }
-                const float absmax = m;
-                const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
-                float y[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) y[k] = r[k] * inv;
-                // a NaN among the scaled residuals makes their sum NaN (otherwise
-                // each is finite and within 7 in magnitude)
-                float t = y[0];
-#pragma unroll
-                for (int k = 1; k < 8; k++) t += y[k];
-                uint32_t word = 0;
-                if (__ballot(!(t == t)) == 0ull) {
-                    // clamp to [-7, 7], then round half to even by adding 1.5 * 2^23
-                    // (unit in the last place 1): the low nibble of the sum's bits
-                    // is the code in two's complement, as quant7 gives it
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        const float c = __builtin_amdgcn_fmed3f(y[k], -7.0f, 7.0f) + 12582912.0f;
-                        word |= (__builtin_bit_cast(uint32_t, c) & 0xFu) << (4 * k);
-                    }
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 8; k++) word |= ((uint32_t)quant7(y[k]) & 0xFu) << (4 * k);
-                }
-                if (live) {
-                    ((uint32_t*)(J.code_plane + dv * (D / 2)))[j] = word;
-                    if (j == 0) J.rscale_plane[dv] = f2h(absmax);
-                }
-            }
+            const EncodeDst dst{J.sign_plane, J.scale_plane, J.code_plane, J.rscale_plane};
+            encode_row<D, MODE>(J.src + v * D, j, live, dst, dv);
         }
     }
 }

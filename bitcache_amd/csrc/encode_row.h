@@ -1,0 +1,153 @@
+// One vector of the row encoder, shared by the encode kernels (encode.hip) and
+// the attention kernel's in-place append (attention_mfma.hip).
+//
+// d in {64, 128, 256}: L = d/8 lanes per vector, lane j (0 <= j < L) of its
+// L-lane group holding elements 8j..8j+7 (one 16-byte load); a wave holds
+// 64/L such groups, lane = group * L + j, and every lane of the wave calls
+// encode_row (the reductions are DPP / swizzle moves within the group).  The
+// scale sum follows the reference tree exactly: element t = 8j + k sits in
+// lane j, so the tree levels s = 64..8 (src/binary_encode.cu:83-88) pair lane
+// j with lane j + s/8 (row_shl) and the levels s = 4, 2, 1 are in-lane; d = 256
+// first adds |x_{t+128}| from the lane 16 above (the reference's per-thread
+// loop, :70-80), d = 64 skips the s = 64 level (it adds +0.0).
+#pragma once
+
+#include "common.h"
+
+namespace bc {
+
+enum EncodeMode : int {
+    ENC_BINARY = 0,         // bits + scale
+    ENC_FUSED_FP16 = 1,     // bits + scale + residual against the fp16 scale (two-step semantics)
+    ENC_FUSED_FP32 = 2,     // bits + scale + residual against the fp32 mean (online semantics)
+    ENC_RESIDUAL_ONLY = 3,  // residual against bits + fp16 scale read from a binary blob
+};
+
+// Planes of a destination blob pair (code_plane may be null: binary only).
+struct EncodeDst {
+    uint8_t* sign_plane;    // ENC_RESIDUAL_ONLY: read, not written
+    uint16_t* scale_plane;
+    uint8_t* code_plane;
+    uint16_t* rscale_plane;
+};
+
+// __float2int_rn followed by the [-7, 7] clamp of src/residual.cu:237-242; NaN -> 0.
+__device__ __forceinline__ int quant7(float v) {
+    if (!(v == v)) return 0;
+    float c = fminf(fmaxf(v, -7.0f), 7.0f);
+    return (int)__builtin_rintf(c);
+}
+
+// Encode the d-element fp16 vector at vec into vector slot dv of dst; lanes
+// with live = false compute along (their group's reductions) but store nothing.
+template <int D, int MODE>
+__device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live, const EncodeDst& dst,
+                                           int64_t dv) {
+    static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
+    constexpr int L = D / 8;        // lanes per vector
+    // swizzle pattern that broadcasts lane 0 of each L-lane group (and-mask mode)
+    constexpr int BCAST = L == 8 ? 0x18 : (L == 16 ? 0x10 : 0x00);
+    // nontemporal: the wave's vectors are one contiguous run read once
+    const bc_v4u raw = __builtin_nontemporal_load((const bc_v4u*)vec + j);
+    const uint32_t hw[4] = {raw[0], raw[1], raw[2], raw[3]};
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) x[k] = h2f((uint16_t)(hw[k >> 1] >> (16 * (k & 1))));
+
+    uint32_t byte = 0;
+    float s;
+    float mean = 0.0f;
+    if constexpr (MODE == ENC_RESIDUAL_ONLY) {
+        byte = dst.sign_plane[dv * (D / 8) + j];
+        s = h2f(dst.scale_plane[dv]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; k++) byte |= (x[k] >= 0.0f ? 1u : 0u) << k;  // +-0 -> 1, NaN -> 0
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]);
+        if constexpr (D == 256) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = p[k] + swz_f<0x401F>(p[k]);  // + |x_{t+128}|
+        }
+        if constexpr (D >= 128) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x108>(p[k]);   // s = 64
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);       // s = 32
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x102>(p[k]);       // s = 16
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x101>(p[k]);       // s = 8
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = p[k] + p[k + 4];                  // s = 4
+        p[0] = p[0] + p[2];
+        p[1] = p[1] + p[3];                                                   // s = 2
+        p[0] = p[0] + p[1];                                                   // s = 1
+        const float total_abs = swz_f<BCAST>(p[0]);
+        mean = total_abs / (float)D;
+        if constexpr (MODE == ENC_FUSED_FP16) s = h2f(f2h(mean));
+        else s = mean;
+        // sign bytes of 4 lanes -> one little-endian word
+        const uint32_t w = byte | (dpp_u<0x101>(byte) << 8) | (dpp_u<0x102>(byte) << 16) |
+                           (dpp_u<0x103>(byte) << 24);
+        if (live) {
+            if ((j & 3) == 0) ((uint32_t*)(dst.sign_plane + dv * (D / 8)))[j >> 2] = w;
+            if (j == 0) dst.scale_plane[dv] = f2h(mean);
+        }
+    }
+
+    if constexpr (MODE != ENC_BINARY) {
+        if (dst.code_plane == nullptr) return;
+        float r[8];
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            r[k] = x[k] - (((byte >> k) & 1u) ? s : -s);
+            m = fmaxf(m, fabsf(r[k]));
+        }
+        // fmaxf ignores NaN and is order independent (src/residual.cu:201-223)
+        if constexpr (L == 8) {
+            m = fmaxf(m, dpp_f<0x141>(m));   // half mirror
+            m = fmaxf(m, dpp_f<0x4E>(m));    // quad 2,3,0,1
+            m = fmaxf(m, dpp_f<0xB1>(m));    // quad 1,0,3,2
+        } else {
+            m = fmaxf(m, dpp_f<0x128>(m));   // row rotations
+            m = fmaxf(m, dpp_f<0x124>(m));
+            m = fmaxf(m, dpp_f<0x122>(m));
+            m = fmaxf(m, dpp_f<0x121>(m));
+            if constexpr (L == 32) m = fmaxf(m, swz_f<0x401F>(m));
+        }
+        const float absmax = m;
+        const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
+        float y[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) y[k] = r[k] * inv;
+        // a NaN among the scaled residuals makes their sum NaN (otherwise
+        // each is finite and within 7 in magnitude)
+        float t = y[0];
+#pragma unroll
+        for (int k = 1; k < 8; k++) t += y[k];
+        uint32_t word = 0;
+        if (__ballot(!(t == t)) == 0ull) {
+            // clamp to [-7, 7], then round half to even by adding 1.5 * 2^23
+            // (unit in the last place 1): the low nibble of the sum's bits
+            // is the code in two's complement, as quant7 gives it
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float c = __builtin_amdgcn_fmed3f(y[k], -7.0f, 7.0f) + 12582912.0f;
+                word |= (__builtin_bit_cast(uint32_t, c) & 0xFu) << (4 * k);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) word |= ((uint32_t)quant7(y[k]) & 0xFu) << (4 * k);
+        }
+        if (live) {
+            ((uint32_t*)(dst.code_plane + dv * (D / 2)))[j] = word;
+            if (j == 0) dst.rscale_plane[dv] = f2h(absmax);
+        }
+    }
+}
+
+}  // namespace bc

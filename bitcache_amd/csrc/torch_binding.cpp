@@ -234,6 +234,57 @@ torch::Tensor attention(torch::Tensor Q, torch::Tensor K_bin, std::optional<torc
     return out.view(Q.sizes());
 }
 
+// One decode step: append the token (k, v: [batch*n_kv_heads*head_dim] fp16) at
+// position current_len % max_seq of the ring caches, then attend over the
+// filled positions (bc_append_attention).
+torch::Tensor append_attention(torch::Tensor Q, torch::Tensor k, torch::Tensor v,
+                               torch::Tensor K_bin, std::optional<torch::Tensor> K_res,
+                               torch::Tensor V_bin, std::optional<torch::Tensor> V_res,
+                               int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                               int64_t head_dim, int64_t current_len, int64_t max_seq) {
+    check_q(Q, batch, n_heads, head_dim);
+    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "n_heads must be a multiple of n_kv_heads");
+    check_kv_token(k, batch, n_kv_heads, head_dim);
+    check_kv_token(v, batch, n_kv_heads, head_dim);
+    check_same_device(Q, k, "k");
+    check_same_device(Q, v, "v");
+    BC_CHECK_BLOB(K_bin);
+    BC_CHECK_BLOB(V_bin);
+    check_same_device(Q, K_bin, "K_bin");
+    check_same_device(Q, V_bin, "V_bin");
+    TORCH_CHECK(max_seq > 0 && current_len >= 0, "max_seq must be > 0 and current_len >= 0");
+    const int64_t cap = batch * n_kv_heads * max_seq;
+    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
+    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
+    TORCH_CHECK(K_res.has_value() == V_res.has_value(), "K_res and V_res: both or neither");
+    void *kr = nullptr, *vr = nullptr;
+    if (K_res.has_value()) {
+        BC_CHECK_BLOB(*K_res);
+        BC_CHECK_BLOB(*V_res);
+        check_same_device(Q, *K_res, "K_res");
+        check_same_device(Q, *V_res, "V_res");
+        check_blob_size(*K_res, cap, bc_sizeof_residual_vec(), "K_res");
+        check_blob_size(*V_res, cap, bc_sizeof_residual_vec(), "V_res");
+        kr = K_res->data_ptr();
+        vr = V_res->data_ptr();
+    }
+    c10::DeviceGuard guard(Q.device());
+    const int64_t seq_len = current_len + 1 < max_seq ? current_len + 1 : max_seq;
+    size_t ws_bytes = 0;
+    check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
+                                             (int)seq_len, (int)head_dim, &ws_bytes),
+                 "attention_workspace_size");
+    auto ws = workspace_for(Q, ws_bytes);
+    auto out = torch::empty({batch, n_heads, head_dim}, Q.options());
+    check_status(bc_append_attention(Q.data_ptr(), k.data_ptr(), v.data_ptr(), K_bin.data_ptr(), kr,
+                                     V_bin.data_ptr(), vr, out.data_ptr(), (int)batch, (int)n_heads,
+                                     (int)n_kv_heads, (int)head_dim, current_len, (int)max_seq,
+                                     ws.data_ptr(), ws_bytes, stream_of(Q)),
+                 "append_attention");
+    return out.view(Q.sizes());
+}
+
 // Phase 1 only: returns the workspace holding the split partials.
 torch::Tensor attention_partial(torch::Tensor Q, torch::Tensor K_bin,
                                 std::optional<torch::Tensor> K_res, torch::Tensor V_bin,
@@ -461,6 +512,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("online_encode_kv", &online_encode_kv, "K and V token encode in one launch");
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
     m.def("attention", &attention, "GQA / ring-stride binary or compensated attention");
+    m.def("append_attention", &append_attention, "One decode step: ring-cache append + attention");
     m.def("attention_partial", &attention_partial, "Split-KV partials (phase 1 of attention)");
     m.def("attention_combine", &attention_combine, "Merge split-KV partials (phase 2)");
     m.def("adaptive_attention", &adaptive_attention, "Top-k residual selection attention");

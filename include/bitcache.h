@@ -144,6 +144,23 @@ int bc_attention_partial(const void* q, const void* k_bin, const void* k_res, co
 int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads, int n_kv_heads,
                          int seq_len, int head_dim, void* stream);
 
+/* One decode step on ring caches of capacity batch*n_kv_heads*max_seq: the new
+ * token k_new / v_new ([batch*n_kv_heads, head_dim] fp16) is encoded into
+ * position current_len % max_seq of every (b, kv head) row with the
+ * online-encode math, then q attends over the min(current_len + 1, max_seq)
+ * filled positions.  Same cache bytes and output as bc_online_encode_kv
+ * followed by bc_attention_gqa (seq_len = min(current_len + 1, max_seq),
+ * kv_stride = max_seq), and the same workspace; one launch fewer when the
+ * matrix-core kernel runs with one query-head group per kv head.  Replaces
+ * the pair online_encode_token (src/online_encode.cu:122-149) +
+ * compensated_attention (src/compensated_attention.cu:111-134) that
+ * BitCache.append / attend issue (bitcache/__init__.py:95-148).  k_res/v_res
+ * NULL: binary caches and binary attention. */
+int bc_append_attention(const void* q, const void* k_new, const void* v_new, void* k_bin,
+                        void* k_res, void* v_bin, void* v_res, void* out, int batch, int n_heads,
+                        int n_kv_heads, int head_dim, int64_t current_len, int max_seq,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Per-key binary scores xnor_dot * 1/sqrt(d) (float32 [batch, n_heads, seq_len])
  * and/or the XNOR popcounts (int32, same shape); either output may be NULL.
  * Bit-exact.  Exposes the score of src/xnor_dot.cuh:163-180 /

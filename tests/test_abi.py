@@ -91,6 +91,14 @@ def test_attention_argument_errors(lib):
     a = lib.bc_adaptive_attention
     a.argtypes = [P] * 7 + [ctypes.c_int] * 7 + [P, size_t, P]
     assert a(fake, fake, fake, fake, fake, fake, None, 1, 4, 4, 100, 100, 128, -1, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
+    f = lib.bc_append_attention
+    f.argtypes = [P] * 8 + [ctypes.c_int] * 4 + [ctypes.c_int64, ctypes.c_int, P, size_t, P]
+    assert f(*[fake] * 4, fake, fake, None, fake, 1, 4, 4, 128, 0, 16, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
+    assert f(*[fake] * 8, 1, 4, 4, 128, 0, 0, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT    # max_seq 0
+    assert f(*[fake] * 8, 1, 4, 4, 128, -1, 16, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT  # current_len < 0
+    assert f(*[fake] * 8, 1, 6, 4, 128, 0, 16, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT   # 6 % 4 != 0
+    assert f(*[fake] * 8, 1, 4, 4, 100, 0, 16, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
+    assert f(*[fake] * 8, 1, 4, 4, 128, 5, 16, fake, 1, None) == BC_ERR_WORKSPACE   # before the token is written
     r = lib.bc_reference_attention
     r.argtypes = [P] * 4 + [ctypes.c_int] * 5 + [P, size_t, P]
     assert r(fake, fake, fake, fake, 1, 4, 4, 100, 96, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED

@@ -139,3 +139,41 @@ def test_config_c4_full_size():
             ref = O.compensated_attention(qg, *enc, 1, G, n, n_kv_heads=1, return_f32=True)[1]
             close(to_np(o[b, kvh * G:(kvh + 1) * G]).astype(np.float32), ref[0],
                   what=f"c4 step {t} group {(b, kvh)}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,d,max_seq,prefill,steps,comp", [
+    (2, 8, 8, 128, 700, 500, 40, True),      # MHA, fused
+    (2, 8, 2, 128, 300, 250, 90, True),      # GQA 4 (the c4 group), fused, wraps at step 50
+    (1, 16, 1, 128, 200, 150, 60, True),     # group 16: two query-head groups, two-launch path
+    (2, 4, 2, 64, 130, 64, 80, False),       # binary caches, d = 64, wraps
+    (1, 4, 4, 256, 96, 0, 120, True),        # d = 256, from empty, wraps
+])
+def test_append_attend_equals_append_then_attend(B, Hq, Hkv, d, max_seq, prefill, steps, comp):
+    """BitCache.append_attend (one launch: the workgroup holding the ring slot
+    encodes the token before attending) leaves the same cache bytes and returns
+    the same output, bit for bit, as append() followed by attend(), at every
+    step, before and after the ring wraps."""
+    from bitcache_amd import BitCache
+    say(f"case append_attend B={B} Hq={Hq} Hkv={Hkv} d={d} max_seq={max_seq} prefill={prefill} "
+        f"steps={steps} comp={comp}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(B * 1000 + steps)
+    rnd = lambda *s: (torch.randn(s, generator=g, device="cuda") * 0.2).half()
+    a = BitCache(B, Hq, d, max_seq, compensated=comp, n_kv_heads=Hkv)
+    b = BitCache(B, Hq, d, max_seq, compensated=comp, n_kv_heads=Hkv)
+    if prefill:
+        k0, v0 = rnd(B, Hkv, prefill, d), rnd(B, Hkv, prefill, d)
+        a.prefill(k0, v0)
+        b.prefill(k0, v0)
+    for t in range(steps):
+        k, v, q = rnd(B, Hkv, d), rnd(B, Hkv, d), rnd(B, Hq, d)
+        a.append(k, v)
+        want = a.attend(q)
+        got = b.append_attend(k, v, q)
+        assert torch.equal(got, want), f"output differs at step {t}"
+        assert a.seq_len == b.seq_len
+    pairs = [(a._k_bin, b._k_bin), (a._v_bin, b._v_bin)]
+    if comp:
+        pairs += [(a._k_res, b._k_res), (a._v_res, b._v_res)]
+    for x, y in pairs:
+        assert torch.equal(x, y)
