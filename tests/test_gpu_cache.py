@@ -96,11 +96,13 @@ def test_bitcache_rejects_bad_inputs():
 
 def test_config_c4_full_size():
     """Config c4 at full size (B4, GQA 32/8, 16384-token prefill + 256 decode
-    steps of append + attend, as bench.py runs it).  Size-independent checks:
-    the cache after the loop is bit-identical to a one-shot prefill of all
-    16640 tokens (appends == prefill), and the outputs of the first, middle and
-    last steps for two head groups match the oracle (online encode of the
-    group's tokens, then compensated attention over them)."""
+    steps of append + attend).  Size-independent checks: the one-launch step
+    (append_attend, as bench.py runs it) gives the same output at every step
+    and the same cache bytes as append() + attend(); the cache after the loop
+    is bit-identical to a one-shot prefill of all 16640 tokens (appends ==
+    prefill); the outputs of the first, middle and last steps for two head
+    groups match the oracle (online encode of the group's tokens, then
+    compensated attention over them)."""
     from bitcache_amd import BitCache
     from bitcache_amd import workloads as W
     say("case c4 full size")
@@ -114,14 +116,20 @@ def test_config_c4_full_size():
     ks = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
     vs = (torch.randn((T, B, Hkv, d), generator=g, device="cuda") * W.SIGMA).half()
     cache = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
+    fused = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)    # the same loop with append_attend
     cache.prefill(k, v)
+    fused.prefill(k, v)
     outs = {}
     for t in range(T):
         cache.append(ks[t], vs[t])
         o = cache.attend(qs[t])
+        assert torch.equal(fused.append_attend(ks[t], vs[t], qs[t]), o), f"append_attend differs at step {t}"
         if t in (0, T // 2, T - 1):
             outs[t] = o.clone()
-    assert cache.seq_len == S + T
+    assert cache.seq_len == fused.seq_len == S + T
+    for x, y in ((cache._k_bin, fused._k_bin), (cache._v_bin, fused._v_bin),
+                 (cache._k_res, fused._k_res), (cache._v_res, fused._v_res)):
+        assert torch.equal(x, y)
     kall = torch.cat([k, ks.permute(1, 2, 0, 3)], dim=2).contiguous()
     vall = torch.cat([v, vs.permute(1, 2, 0, 3)], dim=2).contiguous()
     once = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
