@@ -155,6 +155,7 @@ def test_config_c4_full_size():
     (1, 16, 1, 128, 200, 150, 60, True),     # group 16: two query-head groups, two-launch path
     (2, 4, 2, 64, 130, 64, 80, False),       # binary caches, d = 64, wraps
     (1, 4, 4, 256, 96, 0, 120, True),        # d = 256, from empty, wraps
+    (1, 4, 2, 96, 64, 30, 50, True),         # d = 96: VALU kernels, two-launch path, wraps
 ])
 def test_append_attend_equals_append_then_attend(B, Hq, Hkv, d, max_seq, prefill, steps, comp):
     """BitCache.append_attend (one launch: the workgroup holding the ring slot
