@@ -590,10 +590,12 @@ void attn_mfma_kernel(AttnArgs a) {
     };
 
     // ---------------- adaptive mode: a tile's selection, from its stored
-    // popcounts and K scales, and the loads of its residual data (K codes and
-    // residual scales to registers, V codes with the V signs to staging buffer
-    // buf).  The lanes of keys no head selected load from past the range
-    // (zeros, no traffic), so the loads issue without branches.
+    // popcounts and K scales, and the loads of its residual data: the residual
+    // scales per key (lane = key), the K codes and V codes of the selected keys
+    // at their compacted positions (K codes to registers, V codes to staging
+    // buffer buf with the V signs).  Unselected keys and the positions past
+    // the selected ones load from past the range (zeros, no traffic), so the
+    // loads issue without branches.
     auto gather = [&](KRegs<D>& r, int t0, int buf) {
         const int s = t0 + kown;
         const bool valid = s < key_end;
