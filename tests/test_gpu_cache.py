@@ -186,3 +186,39 @@ def test_append_attend_equals_append_then_attend(B, Hq, Hkv, d, max_seq, prefill
         pairs += [(a._k_res, b._k_res), (a._v_res, b._v_res)]
     for x, y in pairs:
         assert torch.equal(x, y)
+
+
+def test_append_attend_in_a_hip_graph():
+    """A decode loop of append_attend steps captured in one HIP graph: three
+    replays, each from the same prefilled cache with eager work and a
+    synchronisation in between, give the eager outputs and cache bytes bit for
+    bit (the ops allocate only from torch's graph pool and record no memset)."""
+    from bitcache_amd import BitCache
+    say("case append_attend graph")
+    B, Hq, Hkv, d, S, T = 2, 8, 2, 128, 600, 24
+    g = torch.Generator(device="cuda")
+    g.manual_seed(21)
+    rnd = lambda *s: (torch.randn(s, generator=g, device="cuda") * 0.2).half()
+    k0, v0 = rnd(B, Hkv, S, d), rnd(B, Hkv, S, d)
+    ks, vs, qs = rnd(T, B, Hkv, d), rnd(T, B, Hkv, d), rnd(T, B, Hq, d)
+    cache = BitCache(B, Hq, d, S + T, n_kv_heads=Hkv)
+
+    def start():
+        cache.reset()
+        cache.prefill(k0, v0)
+        torch.cuda.synchronize()
+
+    start()
+    want = [cache.append_attend(ks[t], vs[t], qs[t]).clone() for t in range(T)]
+    want_k = cache._k_res.clone()
+    start()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = [cache.append_attend(ks[t], vs[t], qs[t]) for t in range(T)]
+    for rep in range(3):
+        start()
+        graph.replay()
+        torch.cuda.synchronize()
+        for t in range(T):
+            assert torch.equal(got[t], want[t]), f"replay {rep}, step {t}"
+        assert torch.equal(cache._k_res, want_k), f"replay {rep}: cache bytes"
