@@ -18,6 +18,9 @@
  *   residual blob [0, n*d/2)        INT4 codes of vector v at v*d/2, element 2j in
  *                                   the low nibble of byte j (as the reference)
  *                 [n*d/2, +2n)      fp16 residual absmax of vector v at n*d/2 + 2v
+ * The bytes past these planes (up to n*36 and n*130) are unused: no encoder
+ * writes them and no kernel reads them, so their content is whatever the
+ * caller's allocation held.
  * The capacity n of a blob is implied by each entry point (documented per
  * function).  bc_binary_to_reference()/..._from_reference() convert to and from
  * the reference's array-of-structs bytes.
