@@ -26,6 +26,7 @@ using bc::kLog2e;
 using bc::MODE_BINARY;
 using bc::MODE_COMP;
 using bc::MODE_ADAPTIVE;
+using bc::MODE_MIXED;
 
 namespace {
 
@@ -833,7 +834,7 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
 // attention one round of what fits of their kernel, at most three workgroups
 // per CU (the adaptive kernel's LDS allows two at d = 128).
 int plan_per_cu(int mode, int D, int G) {
-    if (mode == MODE_COMP && G == 1) return 0;
+    if ((mode == MODE_COMP || mode == MODE_MIXED) && G == 1) return 0;
     const int n = bc::mfma_wgs_per_cu(mode, D, G);
     return n <= 0 ? 3 : (n < 3 ? n : 3);
 }
@@ -922,7 +923,8 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
                 const void* v_res, int batch, int n_heads, int n_kv_heads, int seq_len,
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
                 hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
-                uint8_t* selected, const void* pcs, int per_cu, const AppendArgs* app = nullptr) {
+                uint8_t* selected, const void* pcs, int per_cu, const AppendArgs* app = nullptr,
+                const uint8_t* head_mode = nullptr) {
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -952,6 +954,7 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.cutoff = cutoff;
     a.selected = selected;
     a.pcs = pcs;
+    a.head_mode = head_mode;
     if (app != nullptr) {
         a.app_k = (const uint16_t*)app->k;
         a.app_v = (const uint16_t*)app->v;
@@ -964,6 +967,8 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
         return bc::check_launch("attention split (mfma)");
     // (the VALU kernel does not append; the append entry point checks first)
     BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
+    BC_REQUIRE(mode != MODE_MIXED, BC_ERR_UNSUPPORTED,
+               "per-head modes need the MFMA kernel (head_dim 64, 128 or 256)");
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }
@@ -984,12 +989,13 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
-                  const int32_t* cutoff, uint8_t* selected, const void* pcs, const AppendArgs* app) {
+                  const int32_t* cutoff, uint8_t* selected, const void* pcs, const AppendArgs* app,
+                  const uint8_t* head_mode) {
     const int per_cu = head_dim > 0 && n_kv_heads > 0
                            ? plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads)) : kPlanFixed;
     int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
                          kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
-                         selected, pcs, per_cu, app);
+                         selected, pcs, per_cu, app, head_mode);
     if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
@@ -1102,6 +1108,26 @@ extern "C" int bc_append_attention(const void* q, const void* k_new, const void*
     return bc::run_attention(mode, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads,
                              seq_len, max_seq, head_dim, workspace, workspace_bytes, st, nullptr,
                              nullptr, nullptr, nullptr, &app);
+}
+
+// Per-head mode dispatch (the reference's adaptive-precision intent,
+// src/adaptive_precision.cuh:6-49, examples/generation_demo.py:129-141): head
+// (b, h) is attended in binary mode where modes[b*n_heads + h] == 0 (as
+// bc_adaptive_select writes for a high-entropy head) and in compensated mode
+// otherwise, in one launch over the compensated cache.
+extern "C" int bc_head_mode_attention(const void* q, const void* k_bin, const void* k_res,
+                                      const void* v_bin, const void* v_res, const uint8_t* modes,
+                                      void* out, int batch, int n_heads, int n_kv_heads, int seq_len,
+                                      int kv_stride, int head_dim, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    BC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, BC_ERR_UNSUPPORTED,
+               "per-head modes: head_dim 64, 128 or 256, got %d", head_dim);
+    BC_REQUIRE(k_res && v_res, BC_ERR_INVALID_ARGUMENT, "residual blobs required");
+    BC_REQUIRE(modes != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
+               "null modes");
+    return bc::run_attention(MODE_MIXED, q, k_bin, k_res, v_bin, v_res, out, batch, n_heads,
+                             n_kv_heads, seq_len, kv_stride, head_dim, workspace, workspace_bytes,
+                             (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr, nullptr, modes);
 }
 
 template <int D>

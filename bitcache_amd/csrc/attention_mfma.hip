@@ -34,6 +34,7 @@ using bc::kLog2e;
 using bc::MODE_ADAPTIVE;
 using bc::MODE_BINARY;
 using bc::MODE_COMP;
+using bc::MODE_MIXED;
 
 namespace {
 
@@ -315,15 +316,17 @@ void attn_mfma_kernel(AttnArgs a) {
     // lane holds 16-byte code pieces of 16 keys instead of one key's row
     constexpr bool KMF = G > 1 && RES && D >= 128;
     constexpr int NPC = D / 128;  // 16-byte pieces per lane per 16-key block
-    constexpr bool LIN_K = (BC_LIN_K || G > 1) && MODE == MODE_COMP && !KMF;
-    constexpr bool LIN_V = BC_LIN_V && MODE == MODE_COMP;
+    // every key's residual data is read (compensated, and mixed per-head modes)
+    constexpr bool ALLRES = MODE == MODE_COMP || MODE == MODE_MIXED;
+    constexpr bool LIN_K = (BC_LIN_K || G > 1) && ALLRES && !KMF;
+    constexpr bool LIN_V = BC_LIN_V && ALLRES;
     constexpr int Q = D / 32;    // 16-byte pieces per code row
     // Vector-memory operations issued per prefetched tile, counted at their
     // fewest (a load moves at most 16 bytes; planes are separate loads), so
     // waiting down to this many outstanding operations completes everything
     // issued before the prefetch and never less.
     constexpr int kSignDma = SB >= 16 ? SB / 16 : 1;
-    constexpr int kVDma = kSignDma + (MODE == MODE_COMP ? Q : 0);
+    constexpr int kVDma = kSignDma + (ALLRES ? Q : 0);
     constexpr int kKLoads = (SB + 15) / 16 + (RES ? 4 + Q : 2);
     constexpr int kPrefetchOps = kVDma + kKLoads;
     static_assert(kPrefetchOps + kVDma < 64, "vmcnt holds 6 bits");
@@ -453,6 +456,14 @@ void attn_mfma_kernel(AttnArgs a) {
             thr_value[g] = key_value(thresh[g]);
         }
     }
+    // mixed mode: which heads of the group add their residual
+    bool hmode[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) hmode[g] = true;
+    if constexpr (MODE == MODE_MIXED) {
+#pragma unroll
+        for (int g = 0; g < G; g++) hmode[g] = a.head_mode[bhq0 + g] != 0;
+    }
 
     // query digits of a single head in scalar registers for the whole loop
     // (uniform operands of v_dot8) when codes are read per key, and the int8
@@ -579,7 +590,7 @@ void attn_mfma_kernel(AttnArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs), 16,
                                                      tr * SB + 16 * (lane & 31), 0, 0, 0);
         }
-        if constexpr (MODE == MODE_COMP) {
+        if constexpr (ALLRES) {
 #pragma unroll
             for (int c = 0; c < Q; c++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -822,7 +833,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 racc[0] = s0 + 16 * s1 + 256 * s2 + 4096 * s3;
             }
         } else if constexpr (RES) {
-            bool any_res = MODE == MODE_COMP;
+            bool any_res = ALLRES;
             if constexpr (MODE == MODE_ADAPTIVE) any_res = selmask != 0u;
             if (any_res) {
                 int sa[G][4];
@@ -853,6 +864,7 @@ void attn_mfma_kernel(AttnArgs a) {
             float score = xd[g];
             bool use_res = MODE == MODE_COMP;
             if constexpr (MODE == MODE_ADAPTIVE) use_res = (selmask >> g) & 1u;
+            if constexpr (MODE == MODE_MIXED) use_res = hmode[g];
             // (the matrix-core dots come x16, an exact power of two)
             if (RES && use_res)
                 score = score + (float)racc[g] * (qd.dq[g] * (rsk * (KMF ? 1.0f / 112.0f : 1.0f / 7.0f)));
@@ -928,6 +940,10 @@ void attn_mfma_kernel(AttnArgs a) {
             if constexpr (MODE == MODE_COMP) {
                 bv = p * fb;
                 fo = fo_res;
+            }
+            if constexpr (MODE == MODE_MIXED) {
+                bv = hmode[g] ? p * fb : 0.0f;
+                fo = hmode[g] ? fo_res : fo_bin;
             }
             if constexpr (MODE == MODE_ADAPTIVE) {
                 const bool selg = (selmask >> g) & 1u;
@@ -1241,6 +1257,8 @@ void launch_dg(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_BINARY>), grid, dim3(256), 0, st, a);
     else if (mode == MODE_COMP)
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_COMP>), grid, dim3(256), 0, st, a);
+    else if (mode == MODE_MIXED)
+        hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_MIXED>), grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_ADAPTIVE>), grid, dim3(256), 0, st, a);
 }
@@ -1263,6 +1281,8 @@ int occupancy_dg(int mode) {
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_BINARY>, 256, 0);
     else if (mode == MODE_COMP)
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_COMP>, 256, 0);
+    else if (mode == MODE_MIXED)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_MIXED>, 256, 0);
     else
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_kernel<D, G, MODE_ADAPTIVE>, 256, 0);
     return e == hipSuccess ? n : 0;

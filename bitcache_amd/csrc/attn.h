@@ -8,7 +8,10 @@ namespace bc {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-enum AttnMode : int { MODE_BINARY = 0, MODE_COMP = 1, MODE_ADAPTIVE = 2 };
+// MODE_MIXED: compensated data flow, each (b, query head) adding its residual
+// (score and value) or not as head_mode says: per-head binary / compensated
+// dispatch in one launch.
+enum AttnMode : int { MODE_BINARY = 0, MODE_COMP = 1, MODE_ADAPTIVE = 2, MODE_MIXED = 3 };
 
 struct AttnArgs {
     const uint16_t* q;  // [B, Hq, D] fp16
@@ -32,6 +35,8 @@ struct AttnArgs {
     const uint16_t* app_k;
     const uint16_t* app_v;
     int app_slot;
+    // MODE_MIXED: [B*Hq] 0 = binary attention for that head, else compensated
+    const uint8_t* head_mode;
 };
 
 // Packs per row of the stored popcounts: S rounded up to 16, so that every
@@ -74,6 +79,6 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   int seq_len, int kv_stride, int head_dim, void* workspace,
                   size_t workspace_bytes, hipStream_t st, const uint32_t* thresh,
                   const int32_t* cutoff, uint8_t* selected, const void* pcs,
-                  const AppendArgs* app = nullptr);
+                  const AppendArgs* app = nullptr, const uint8_t* head_mode = nullptr);
 size_t attention_ws_bytes(int batch, int n_heads, int n_kv_heads, int seq_len, int d);
 }  // namespace bc

@@ -234,6 +234,46 @@ torch::Tensor attention(torch::Tensor Q, torch::Tensor K_bin, std::optional<torc
     return out.view(Q.sizes());
 }
 
+// Per-head binary / compensated dispatch in one launch (bc_head_mode_attention):
+// modes uint8 [batch, n_heads], 0 = binary for that head.
+torch::Tensor head_mode_attention(torch::Tensor Q, torch::Tensor K_bin, torch::Tensor K_res,
+                                  torch::Tensor V_bin, torch::Tensor V_res, torch::Tensor modes,
+                                  int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                                  int64_t seq_len, int64_t kv_stride, int64_t head_dim) {
+    check_q(Q, batch, n_heads, head_dim);
+    for (const auto* t : {&K_bin, &K_res, &V_bin, &V_res}) {
+        BC_CHECK_BLOB(*t);
+        check_same_device(Q, *t, "cache blob");
+    }
+    BC_CHECK_DEV(modes);
+    BC_CHECK_CONTIG(modes);
+    BC_CHECK_U8(modes);
+    check_same_device(Q, modes, "modes");
+    TORCH_CHECK(modes.numel() == batch * n_heads, "modes must hold batch*n_heads values");
+    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "n_heads must be a multiple of n_kv_heads");
+    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
+    const int64_t cap = batch * n_kv_heads * kv_stride;
+    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
+    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
+    check_blob_size(K_res, cap, bc_sizeof_residual_vec(), "K_res");
+    check_blob_size(V_res, cap, bc_sizeof_residual_vec(), "V_res");
+    c10::DeviceGuard guard(Q.device());
+    size_t ws_bytes = 0;
+    check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
+                                             (int)seq_len, (int)head_dim, &ws_bytes),
+                 "attention_workspace_size");
+    auto ws = workspace_for(Q, ws_bytes);
+    auto out = torch::empty({batch, n_heads, head_dim}, Q.options());
+    check_status(bc_head_mode_attention(Q.data_ptr(), K_bin.data_ptr(), K_res.data_ptr(),
+                                        V_bin.data_ptr(), V_res.data_ptr(),
+                                        modes.data_ptr<uint8_t>(), out.data_ptr(), (int)batch,
+                                        (int)n_heads, (int)n_kv_heads, (int)seq_len, (int)kv_stride,
+                                        (int)head_dim, ws.data_ptr(), ws_bytes, stream_of(Q)),
+                 "head_mode_attention");
+    return out.view(Q.sizes());
+}
+
 // One decode step: append the token (k, v: [batch*n_kv_heads*head_dim] fp16) at
 // position current_len % max_seq of the ring caches, then attend over the
 // filled positions (bc_append_attention).
@@ -513,6 +553,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
     m.def("attention", &attention, "GQA / ring-stride binary or compensated attention");
     m.def("append_attention", &append_attention, "One decode step: ring-cache append + attention");
+    m.def("head_mode_attention", &head_mode_attention, "Per-head binary / compensated attention");
     m.def("attention_partial", &attention_partial, "Split-KV partials (phase 1 of attention)");
     m.def("attention_combine", &attention_combine, "Merge split-KV partials (phase 2)");
     m.def("adaptive_attention", &adaptive_attention, "Top-k residual selection attention");

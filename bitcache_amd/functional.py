@@ -120,6 +120,31 @@ def adaptive_select(entropy: Tensor, threshold: float) -> Tensor:
     return _C.adaptive_select(entropy, threshold)
 
 
+def head_mode_attention(Q: Tensor, K_bin: Tensor, K_res: Tensor, V_bin: Tensor, V_res: Tensor,
+                        modes: Tensor, batch: int, n_heads: int, seq_len: int, head_dim: int, *,
+                        n_kv_heads: Optional[int] = None, kv_stride: Optional[int] = None) -> Tensor:
+    """Binary attention for the heads with modes[b, h] == 0, compensated attention for the
+    others, in one launch (the per-head intent of src/adaptive_precision.cuh:6-49).
+    modes: uint8 [batch, n_heads], as adaptive_select returns it."""
+    _require_extension()
+    _check_q(Q)
+    return _C.head_mode_attention(Q, K_bin, K_res, V_bin, V_res, modes.contiguous(), batch,
+                                  n_heads, n_heads if n_kv_heads is None else n_kv_heads, seq_len,
+                                  seq_len if kv_stride is None else kv_stride, head_dim)
+
+
+def entropy_dispatch_attention(Q: Tensor, K_bin: Tensor, K_res: Tensor, V_bin: Tensor,
+                               V_res: Tensor, batch: int, n_heads: int, seq_len: int,
+                               head_dim: int, threshold: float) -> Tuple[Tensor, Tensor]:
+    """The reference's adaptive precision end to end (MHA): per-head entropy of the binary
+    scores (src/adaptive_precision.cu:13-130), mode = binary where entropy >= threshold
+    (:133-144), then head_mode_attention.  Returns (out, modes)."""
+    ent = compute_head_entropy(Q, K_bin, batch, n_heads, seq_len, head_dim)
+    modes = adaptive_select(ent, threshold).view(batch, n_heads)
+    return head_mode_attention(Q, K_bin, K_res, V_bin, V_res, modes, batch, n_heads, seq_len,
+                               head_dim), modes
+
+
 def reference_attention(Q: Tensor, K: Tensor, V: Tensor, batch: int, n_heads: int, seq_len: int,
                         head_dim: int, *, n_kv_heads: Optional[int] = None) -> Tensor:
     """Exact fp16 attention, fp32 accumulation (src/reference_attention.cu)."""

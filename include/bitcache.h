@@ -147,6 +147,18 @@ int bc_attention_partial(const void* q, const void* k_bin, const void* k_res, co
 int bc_attention_combine(const void* workspace, void* out, int batch, int n_heads, int n_kv_heads,
                          int seq_len, int head_dim, void* stream);
 
+/* Per-head binary / compensated dispatch in one launch over a compensated cache:
+ * head (b, h) is attended like bc_attention_gqa with k_res/v_res NULL where
+ * modes[b*n_heads + h] == 0 and with them otherwise (modes as written by
+ * bc_adaptive_select from bc_compute_head_entropy).  The reference's intent
+ * for adaptive precision (src/adaptive_precision.cuh:6-49), which its demo
+ * dispatches per layer in Python (examples/generation_demo.py:129-141).
+ * head_dim 64, 128 or 256; workspace as bc_attention_workspace_size. */
+int bc_head_mode_attention(const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                           const void* v_res, const uint8_t* modes, void* out, int batch,
+                           int n_heads, int n_kv_heads, int seq_len, int kv_stride, int head_dim,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* One decode step on ring caches of capacity batch*n_kv_heads*max_seq: the new
  * token k_new / v_new ([batch*n_kv_heads, head_dim] fp16) is encoded into
  * position current_len % max_seq of every (b, kv head) row with the

@@ -257,3 +257,66 @@ def test_gqa_equals_mha_on_repeated_kv(F, group, d):
             m = F.binary_attention(qt, kbm, vbm, B, Hq, S, d)
         close(to_np(g).astype(np.float32), to_np(m).astype(np.float32),
               what=f"gqa vs mha group={group} d={d} comp={comp}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,d", [(2, 8, 8, 1500, 128), (2, 16, 4, 2000, 128),
+                                          (1, 8, 2, 900, 64), (1, 4, 4, 700, 256)])
+def test_head_mode_attention(F, B, Hq, Hkv, S, d):
+    """Per-head dispatch in one launch: heads with mode 0 match the oracle's
+    binary attention, heads with mode 1 its compensated attention (modes mixed
+    inside GQA groups); all-compensated modes agree with compensated attention
+    to rounding (the same arithmetic, which the compiler may contract into
+    FMAs differently in the two kernels)."""
+    say(f"case head modes B={B} Hq={Hq} Hkv={Hkv} S={S} d={d}")
+    q, k, v = make(B, Hq, Hkv, S, d, seed=S + d, lognorm=0.25)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    rng = np.random.default_rng(S)
+    modes = rng.integers(0, 2, size=(B, Hq)).astype(np.uint8)
+    modes[0, 0], modes[-1, -1] = 0, 1
+    out = to_np(F.head_mode_attention(qt, kb, kr, vb, vr, torch.from_numpy(modes).cuda(), B, Hq, S, d,
+                                      n_kv_heads=Hkv)).astype(np.float32)
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, rb = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    _, rc = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    for b in range(B):
+        for h in range(Hq):
+            ref = rc[b, h] if modes[b, h] else rb[b, h]
+            close(out[b, h], ref, what=f"head ({b}, {h}) mode {modes[b, h]}")
+    ones = torch.ones((B, Hq), dtype=torch.uint8, device="cuda")
+    allc = F.head_mode_attention(qt, kb, kr, vb, vr, ones, B, Hq, S, d, n_kv_heads=Hkv)
+    comp = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
+    close(to_np(allc).astype(np.float32), to_np(comp).astype(np.float32), rel=1e-3, cos=0.999999,
+          what="all heads compensated")
+
+
+def test_entropy_dispatch_attention(F):
+    """The reference's adaptive precision end to end (MHA): entropy per head,
+    mode = binary where entropy >= threshold, one launch; modes and outputs
+    against the oracle."""
+    say("case entropy dispatch")
+    B, H, S, d = 2, 8, 2500, 128
+    q, k, v = make(B, H, H, S, d, seed=31, scale=0.3)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    n = B * H * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    ent = O.head_entropy(q, Kb, B, H, S)
+    thr = float(np.median(ent))
+    out, modes = F.entropy_dispatch_attention(qt, kb, kr, vb, vr, B, H, S, d, thr)
+    modes = to_np(modes)
+    want = (ent < thr).astype(np.uint8).reshape(B, H)
+    # heads within float rounding of the threshold may land either side
+    near = np.abs(ent.reshape(B, H) - thr) <= 2e-4 * max(1.0, abs(thr))
+    assert np.array_equal(modes[~near], want[~near])
+    _, rb = O.binary_attention(q, Kb, Vb, B, H, S, return_f32=True)
+    _, rc = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, H, S, return_f32=True)
+    out = to_np(out).astype(np.float32)
+    for b in range(B):
+        for h in range(H):
+            close(out[b, h], rc[b, h] if modes[b, h] else rb[b, h], what=f"head ({b}, {h})")
