@@ -153,6 +153,26 @@ class BitCache:
                                          return_selected)
         return (out, sel) if return_selected else out
 
+    def attend_head_mode(self, Q: Tensor, threshold: Optional[float] = None,
+                         modes: Optional[Tensor] = None, return_modes: bool = False):
+        """Binary or compensated attention chosen per (batch, query head) in one
+        launch: from ``modes`` (uint8 [batch, n_heads], 0 = binary) or, given a
+        ``threshold``, from the entropy of each head's binary scores over the
+        cached tokens (binary where entropy >= threshold): the reference's
+        adaptive precision (src/adaptive_precision.cuh:6-49).  Needs
+        compensated=True."""
+        assert self.compensated, "per-head modes need the residual buffers"
+        assert self._filled > 0, "cache is empty, call append() first"
+        assert (threshold is None) != (modes is None), "give exactly one of threshold and modes"
+        if modes is None:
+            ent = _C.head_entropy(Q, self._k_bin, self.batch, self.n_heads, self.n_kv_heads,
+                                  self._filled, self.max_seq, self.head_dim)
+            modes = _C.adaptive_select(ent, threshold).view(self.batch, self.n_heads)
+        out = _C.head_mode_attention(Q, self._k_bin, self._k_res, self._v_bin, self._v_res,
+                                     modes.contiguous(), self.batch, self.n_heads,
+                                     self.n_kv_heads, self._filled, self.max_seq, self.head_dim)
+        return (out, modes) if return_modes else out
+
     def reset(self) -> None:
         """Clear the cache (bitcache/__init__.py:150-158)."""
         self._k_bin.zero_()

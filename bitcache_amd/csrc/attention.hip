@@ -668,7 +668,8 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
 constexpr int kEntropyThreads = 1024;
 template <int D>
 __global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t* q, BinPlanes kb,
-                                                                  float* out, int S) {
+                                                                  float* out, int Hq, int Hkv,
+                                                                  int S, int kv_stride) {
     constexpr int NW = kEntropyThreads / 64;
     __shared__ float part[128];
     __shared__ uint32_t qs[D / 32];
@@ -692,7 +693,9 @@ __global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t
         __syncthreads();
     }
     const float sq = part[0] / (float)D;
-    const int64_t base = (int64_t)bh * S;
+    // query head h of batch b reads kv head h / (Hq / Hkv) of that batch
+    const int b = bh / Hq, kvh = (bh % Hq) / (Hq / Hkv);
+    const int64_t base = ((int64_t)b * Hkv + kvh) * kv_stride;
     // online (M, Z, W) per thread over keys tid, tid + T, ...; four keys'
     // loads in flight per thread
     constexpr int U = 4;
@@ -1159,23 +1162,31 @@ extern "C" int bc_binary_scores(const void* q, const void* k_bin, float* scores,
 }
 
 template <int D>
-static void launch_entropy(const void* q, BinPlanes kb, float* out, int bh, int S, hipStream_t st) {
-    hipLaunchKernelGGL((entropy_kernel<D>), dim3(bh), dim3(kEntropyThreads), 0, st, (const uint16_t*)q, kb,
-                       out, S);
+static void launch_entropy(const void* q, BinPlanes kb, float* out, int batch, int hq, int hkv,
+                           int S, int stride, hipStream_t st) {
+    hipLaunchKernelGGL((entropy_kernel<D>), dim3(batch * hq), dim3(kEntropyThreads), 0, st,
+                       (const uint16_t*)q, kb, out, hq, hkv, S, stride);
+}
+
+extern "C" int bc_compute_head_entropy_gqa(const void* q, const void* k_bin, float* entropy,
+                                           int batch, int n_heads, int n_kv_heads, int seq_len,
+                                           int kv_stride, int head_dim, void* stream) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin && entropy, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
+    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
+    BC_DISPATCH_D(head_dim, launch_entropy, q, kb, entropy, batch, n_heads, n_kv_heads, seq_len,
+                  kv_stride, (hipStream_t)stream);
+    return bc::check_launch("entropy");
 }
 
 extern "C" int bc_compute_head_entropy(const void* q, const void* k_bin, float* entropy,
                                        int batch, int n_heads, int seq_len, int head_dim,
                                        void* stream) {
-    int v = validate_heads(batch, n_heads, n_heads > 0 ? n_heads : 1, seq_len, seq_len, head_dim);
-    if (v != BC_OK) return v;
-    if ((int64_t)batch * n_heads == 0) return BC_OK;
-    BC_REQUIRE(q && k_bin && entropy, BC_ERR_INVALID_ARGUMENT, "null pointer");
-    const int64_t cap = (int64_t)batch * n_heads * seq_len;
-    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
-    BC_DISPATCH_D(head_dim, launch_entropy, q, kb, entropy, batch * n_heads, seq_len,
-                  (hipStream_t)stream);
-    return bc::check_launch("entropy");
+    return bc_compute_head_entropy_gqa(q, k_bin, entropy, batch, n_heads, n_heads > 0 ? n_heads : 1,
+                                       seq_len, seq_len, head_dim, stream);
 }
 
 extern "C" int bc_adaptive_select(const float* entropy, uint8_t* modes, int batch, int n_heads,

@@ -42,9 +42,55 @@ void check_same_device(const torch::Tensor& a, const torch::Tensor& b, const cha
     TORCH_CHECK(a.device() == b.device(), name, " must be on the same device as the query/input");
 }
 
-void check_blob_size(const torch::Tensor& blob, int64_t vecs, int64_t per, const char* name) {
-    TORCH_CHECK(blob.numel() >= vecs * per, name, " holds ", blob.numel(), " bytes but ", vecs,
-                " vectors need ", vecs * per);
+// ------------------------------------------------------------------ blob capacity
+// The planar layout puts a blob's scale plane at capacity * d/8 (binary) or
+// capacity * d/2 (residual) bytes, so every op must know the capacity a blob
+// was written with: the size of the allocation it lives in.
+//  - A tensor that starts at its storage's first byte but covers less of it is
+//    a prefix view of a whole blob, as the reference's BitCache.attend slices
+//    its ring buffers (bitcache/__init__.py:134-139): capacity = storage bytes.
+//  - Any other tensor (a whole allocation, or a view at an offset into a
+//    caller's pool) is a blob of its own: capacity = numel / bytes per vector.
+struct Blob {
+    void* base;
+    int64_t cap;
+};
+
+Blob resolve_blob(const torch::Tensor& t, int64_t per, const char* name) {
+    TORCH_CHECK(t.device().is_cuda(), name, " must be a ROCm (cuda) tensor");
+    TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+    TORCH_CHECK(t.scalar_type() == torch::kUInt8, name, " must be uint8");
+    const int64_t stor = (int64_t)t.storage().nbytes();
+    const bool prefix = t.storage_offset() == 0 && t.numel() < stor;
+    const int64_t bytes = prefix ? stor : t.numel();
+    TORCH_CHECK(bytes % per == 0, name, ": ", bytes, prefix ? " bytes of storage" : " bytes",
+                " is not a whole number of ", per, "-byte vectors");
+    return Blob{t.data_ptr(), bytes / per};
+}
+
+// A blob whose capacity must be exactly `vecs` vectors (the layout the op reads or writes).
+void* blob_exact(const torch::Tensor& t, int64_t vecs, int64_t per, const char* name) {
+    const Blob b = resolve_blob(t, per, name);
+    TORCH_CHECK(b.cap == vecs, name, " holds ", b.cap, " vectors of ", per, " bytes but this shape"
+                " needs a blob of exactly ", vecs, " (its planes are laid out for its capacity)");
+    return b.base;
+}
+
+// Reference-signature attention ops (src/torch_binding.cpp:68-117, :141-162)
+// take no stride: keys of row r = b*n_heads + h are read at r*kv_stride + s
+// with kv_stride = capacity / (batch*n_heads).  A blob of exactly
+// batch*n_heads*seq_len vectors gives kv_stride = seq_len (the reference's
+// reading); a prefix view of a ring of max_seq slots per row gives
+// kv_stride = max_seq, the stride the ring was written with
+// (src/online_encode.cu:139), so a partly filled ring reads its own slots.
+int64_t ref_kv_stride(const Blob& b, int64_t batch, int64_t n_heads, int64_t seq_len,
+                      const char* name) {
+    const int64_t rows = batch * n_heads;
+    if (rows == 0) return seq_len;
+    TORCH_CHECK(b.cap % rows == 0 && b.cap / rows >= seq_len && b.cap / rows <= INT32_MAX, name,
+                " holds ", b.cap, " vectors: not batch*n_heads*kv_stride (batch*n_heads = ", rows,
+                ") with kv_stride >= seq_len = ", seq_len);
+    return b.cap / rows;
 }
 
 // ------------------------------------------------------------------ encode
@@ -72,11 +118,11 @@ torch::Tensor residual_encode(torch::Tensor src, torch::Tensor binary_blob) {
     const int64_t d = src.size(1);
     TORCH_CHECK(d % 32 == 0, "head_dim must be a multiple of 32");
     TORCH_CHECK(d <= 256, "head_dim exceeds MAX_HEAD_DIM=256");
-    TORCH_CHECK(binary_blob.numel() == n * bc_sizeof_binary_vec(), "binary_blob size mismatch");
+    void* bin = blob_exact(binary_blob, n, bc_sizeof_binary_vec(), "binary_blob");
     c10::DeviceGuard guard(src.device());
     auto out = torch::empty({n * bc_sizeof_residual_vec()},
                             torch::TensorOptions().dtype(torch::kUInt8).device(src.device()));
-    check_status(bc_residual_encode(src.data_ptr(), binary_blob.data_ptr(), out.data_ptr(), n,
+    check_status(bc_residual_encode(src.data_ptr(), bin, out.data_ptr(), n,
                                     (int)d, stream_of(src)),
                  "residual_encode");
     return out;
@@ -103,24 +149,25 @@ void check_kv_token(const torch::Tensor& kv, int64_t batch, int64_t n_heads, int
     TORCH_CHECK(kv.numel() == batch * n_heads * d, "kv must hold batch*n_heads*head_dim values");
 }
 
+// A residual cache that is the binary cache itself (the reference's binary-mode
+// BitCache passes _k_bin twice, bitcache/__init__.py:104-111) means a binary-only
+// cache: nothing is written as residual (the reference's kernel wrote 130-byte
+// residual records into the 36-byte-per-slot buffer).
 void online_encode_token(torch::Tensor kv, torch::Tensor binary_cache,
                          std::optional<torch::Tensor> residual_cache, int64_t batch,
                          int64_t n_heads, int64_t head_dim, int64_t current_len, int64_t max_seq) {
     check_kv_token(kv, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(binary_cache);
     check_same_device(kv, binary_cache, "binary_cache");
     TORCH_CHECK(max_seq > 0, "max_seq must be > 0");
     const int64_t cap = batch * n_heads * max_seq;
-    check_blob_size(binary_cache, cap, bc_sizeof_binary_vec(), "binary_cache");
+    void* bin = blob_exact(binary_cache, cap, bc_sizeof_binary_vec(), "binary_cache");
     void* res = nullptr;
-    if (residual_cache.has_value()) {
-        BC_CHECK_BLOB(*residual_cache);
+    if (residual_cache.has_value() && !residual_cache->is_alias_of(binary_cache)) {
         check_same_device(kv, *residual_cache, "residual_cache");
-        check_blob_size(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
-        res = residual_cache->data_ptr();
+        res = blob_exact(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
     }
     c10::DeviceGuard guard(kv.device());
-    check_status(bc_online_encode_token(kv.data_ptr(), binary_cache.data_ptr(), res, (int)batch,
+    check_status(bc_online_encode_token(kv.data_ptr(), bin, res, (int)batch,
                                         (int)n_heads, (int)head_dim, current_len, (int)max_seq,
                                         stream_of(kv)),
                  "online_encode_token");
@@ -132,25 +179,19 @@ void online_encode_kv(torch::Tensor k, torch::Tensor v, torch::Tensor k_bin,
                       int64_t head_dim, int64_t current_len, int64_t max_seq) {
     check_kv_token(k, batch, n_heads, head_dim);
     check_kv_token(v, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(k_bin);
-    BC_CHECK_BLOB(v_bin);
     TORCH_CHECK(max_seq > 0, "max_seq must be > 0");
     const int64_t cap = batch * n_heads * max_seq;
-    check_blob_size(k_bin, cap, bc_sizeof_binary_vec(), "k_bin");
-    check_blob_size(v_bin, cap, bc_sizeof_binary_vec(), "v_bin");
+    void* kb = blob_exact(k_bin, cap, bc_sizeof_binary_vec(), "k_bin");
+    void* vb = blob_exact(v_bin, cap, bc_sizeof_binary_vec(), "v_bin");
     TORCH_CHECK(k_res.has_value() == v_res.has_value(), "k_res and v_res: both or neither");
     void *kr = nullptr, *vr = nullptr;
     if (k_res.has_value()) {
-        BC_CHECK_BLOB(*k_res);
-        BC_CHECK_BLOB(*v_res);
-        check_blob_size(*k_res, cap, bc_sizeof_residual_vec(), "k_res");
-        check_blob_size(*v_res, cap, bc_sizeof_residual_vec(), "v_res");
-        kr = k_res->data_ptr();
-        vr = v_res->data_ptr();
+        kr = blob_exact(*k_res, cap, bc_sizeof_residual_vec(), "k_res");
+        vr = blob_exact(*v_res, cap, bc_sizeof_residual_vec(), "v_res");
     }
     c10::DeviceGuard guard(k.device());
-    check_status(bc_online_encode_kv(k.data_ptr(), v.data_ptr(), k_bin.data_ptr(), kr,
-                                     v_bin.data_ptr(), vr, (int)batch, (int)n_heads, (int)head_dim,
+    check_status(bc_online_encode_kv(k.data_ptr(), v.data_ptr(), kb, kr, vb, vr, (int)batch,
+                                     (int)n_heads, (int)head_dim,
                                      current_len, (int)max_seq, stream_of(k)),
                  "online_encode_kv");
 }
@@ -159,22 +200,19 @@ void encode_into_cache(torch::Tensor src, torch::Tensor binary_cache,
                        std::optional<torch::Tensor> residual_cache, int64_t rows, int64_t seq,
                        int64_t head_dim, int64_t start_pos, int64_t max_seq, bool fp32_scale) {
     BC_CHECK_INPUT(src);
-    BC_CHECK_BLOB(binary_cache);
     check_same_device(src, binary_cache, "binary_cache");
     TORCH_CHECK(src.numel() == rows * seq * head_dim, "src must be [rows, seq, head_dim]");
     TORCH_CHECK(max_seq > 0 && start_pos >= 0 && start_pos + seq <= max_seq,
                 "start_pos + seq must fit in max_seq");
     const int64_t cap = rows * max_seq;
-    check_blob_size(binary_cache, cap, bc_sizeof_binary_vec(), "binary_cache");
+    void* bin = blob_exact(binary_cache, cap, bc_sizeof_binary_vec(), "binary_cache");
     void* res = nullptr;
     if (residual_cache.has_value()) {
-        BC_CHECK_BLOB(*residual_cache);
         check_same_device(src, *residual_cache, "residual_cache");
-        check_blob_size(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
-        res = residual_cache->data_ptr();
+        res = blob_exact(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
     }
     c10::DeviceGuard guard(src.device());
-    check_status(bc_encode_into_cache(src.data_ptr(), binary_cache.data_ptr(), res, rows, (int)seq,
+    check_status(bc_encode_into_cache(src.data_ptr(), bin, res, rows, (int)seq,
                                       (int)head_dim, (int)start_pos, (int)max_seq,
                                       fp32_scale ? 1 : 0, stream_of(src)),
                  "encode_into_cache");
@@ -192,33 +230,43 @@ torch::Tensor workspace_for(const torch::Tensor& Q, size_t bytes) {
                         torch::TensorOptions().dtype(torch::kUInt8).device(Q.device()));
 }
 
+// The four cache blobs of an attention call, each of capacity exactly `cap`
+// vectors; residual pointers are null when the residual blobs are absent.
+struct CachePtrs {
+    void *kb, *kr, *vb, *vr;
+};
+
+CachePtrs cache_blobs(const torch::Tensor& Q, const torch::Tensor& K_bin,
+                      const std::optional<torch::Tensor>& K_res, const torch::Tensor& V_bin,
+                      const std::optional<torch::Tensor>& V_res, int64_t cap) {
+    check_same_device(Q, K_bin, "K_bin");
+    check_same_device(Q, V_bin, "V_bin");
+    CachePtrs c{};
+    c.kb = blob_exact(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
+    c.vb = blob_exact(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
+    TORCH_CHECK(K_res.has_value() == V_res.has_value(), "K_res and V_res: both or neither");
+    if (K_res.has_value()) {
+        check_same_device(Q, *K_res, "K_res");
+        check_same_device(Q, *V_res, "V_res");
+        c.kr = blob_exact(*K_res, cap, bc_sizeof_residual_vec(), "K_res");
+        c.vr = blob_exact(*V_res, cap, bc_sizeof_residual_vec(), "V_res");
+    }
+    return c;
+}
+
+void check_heads(int64_t n_heads, int64_t n_kv_heads, int64_t seq_len, int64_t kv_stride) {
+    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+                "n_heads must be a multiple of n_kv_heads");
+    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
+}
+
 torch::Tensor attention(torch::Tensor Q, torch::Tensor K_bin, std::optional<torch::Tensor> K_res,
                         torch::Tensor V_bin, std::optional<torch::Tensor> V_res, int64_t batch,
                         int64_t n_heads, int64_t n_kv_heads, int64_t seq_len, int64_t kv_stride,
                         int64_t head_dim) {
     check_q(Q, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(K_bin);
-    BC_CHECK_BLOB(V_bin);
-    check_same_device(Q, K_bin, "K_bin");
-    check_same_device(Q, V_bin, "V_bin");
-    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                "n_heads must be a multiple of n_kv_heads");
-    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
-    const int64_t cap = batch * n_kv_heads * kv_stride;
-    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
-    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
-    TORCH_CHECK(K_res.has_value() == V_res.has_value(), "K_res and V_res: both or neither");
-    void *kr = nullptr, *vr = nullptr;
-    if (K_res.has_value()) {
-        BC_CHECK_BLOB(*K_res);
-        BC_CHECK_BLOB(*V_res);
-        check_same_device(Q, *K_res, "K_res");
-        check_same_device(Q, *V_res, "V_res");
-        check_blob_size(*K_res, cap, bc_sizeof_residual_vec(), "K_res");
-        check_blob_size(*V_res, cap, bc_sizeof_residual_vec(), "V_res");
-        kr = K_res->data_ptr();
-        vr = V_res->data_ptr();
-    }
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
+    const CachePtrs c = cache_blobs(Q, K_bin, K_res, V_bin, V_res, batch * n_kv_heads * kv_stride);
     c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
@@ -226,10 +274,9 @@ torch::Tensor attention(torch::Tensor Q, torch::Tensor K_bin, std::optional<torc
                  "attention_workspace_size");
     auto ws = workspace_for(Q, ws_bytes);
     auto out = torch::empty({batch, n_heads, head_dim}, Q.options());
-    check_status(bc_attention_gqa(Q.data_ptr(), K_bin.data_ptr(), kr, V_bin.data_ptr(), vr,
-                                  out.data_ptr(), (int)batch, (int)n_heads, (int)n_kv_heads,
-                                  (int)seq_len, (int)kv_stride, (int)head_dim, ws.data_ptr(),
-                                  ws_bytes, stream_of(Q)),
+    check_status(bc_attention_gqa(Q.data_ptr(), c.kb, c.kr, c.vb, c.vr, out.data_ptr(), (int)batch,
+                                  (int)n_heads, (int)n_kv_heads, (int)seq_len, (int)kv_stride,
+                                  (int)head_dim, ws.data_ptr(), ws_bytes, stream_of(Q)),
                  "attention");
     return out.view(Q.sizes());
 }
@@ -241,23 +288,13 @@ torch::Tensor head_mode_attention(torch::Tensor Q, torch::Tensor K_bin, torch::T
                                   int64_t batch, int64_t n_heads, int64_t n_kv_heads,
                                   int64_t seq_len, int64_t kv_stride, int64_t head_dim) {
     check_q(Q, batch, n_heads, head_dim);
-    for (const auto* t : {&K_bin, &K_res, &V_bin, &V_res}) {
-        BC_CHECK_BLOB(*t);
-        check_same_device(Q, *t, "cache blob");
-    }
     BC_CHECK_DEV(modes);
     BC_CHECK_CONTIG(modes);
     BC_CHECK_U8(modes);
     check_same_device(Q, modes, "modes");
     TORCH_CHECK(modes.numel() == batch * n_heads, "modes must hold batch*n_heads values");
-    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                "n_heads must be a multiple of n_kv_heads");
-    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
-    const int64_t cap = batch * n_kv_heads * kv_stride;
-    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
-    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
-    check_blob_size(K_res, cap, bc_sizeof_residual_vec(), "K_res");
-    check_blob_size(V_res, cap, bc_sizeof_residual_vec(), "V_res");
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
+    const CachePtrs c = cache_blobs(Q, K_bin, K_res, V_bin, V_res, batch * n_kv_heads * kv_stride);
     c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
@@ -265,8 +302,7 @@ torch::Tensor head_mode_attention(torch::Tensor Q, torch::Tensor K_bin, torch::T
                  "attention_workspace_size");
     auto ws = workspace_for(Q, ws_bytes);
     auto out = torch::empty({batch, n_heads, head_dim}, Q.options());
-    check_status(bc_head_mode_attention(Q.data_ptr(), K_bin.data_ptr(), K_res.data_ptr(),
-                                        V_bin.data_ptr(), V_res.data_ptr(),
+    check_status(bc_head_mode_attention(Q.data_ptr(), c.kb, c.kr, c.vb, c.vr,
                                         modes.data_ptr<uint8_t>(), out.data_ptr(), (int)batch,
                                         (int)n_heads, (int)n_kv_heads, (int)seq_len, (int)kv_stride,
                                         (int)head_dim, ws.data_ptr(), ws_bytes, stream_of(Q)),
@@ -289,26 +325,8 @@ torch::Tensor append_attention(torch::Tensor Q, torch::Tensor k, torch::Tensor v
     check_kv_token(v, batch, n_kv_heads, head_dim);
     check_same_device(Q, k, "k");
     check_same_device(Q, v, "v");
-    BC_CHECK_BLOB(K_bin);
-    BC_CHECK_BLOB(V_bin);
-    check_same_device(Q, K_bin, "K_bin");
-    check_same_device(Q, V_bin, "V_bin");
     TORCH_CHECK(max_seq > 0 && current_len >= 0, "max_seq must be > 0 and current_len >= 0");
-    const int64_t cap = batch * n_kv_heads * max_seq;
-    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
-    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
-    TORCH_CHECK(K_res.has_value() == V_res.has_value(), "K_res and V_res: both or neither");
-    void *kr = nullptr, *vr = nullptr;
-    if (K_res.has_value()) {
-        BC_CHECK_BLOB(*K_res);
-        BC_CHECK_BLOB(*V_res);
-        check_same_device(Q, *K_res, "K_res");
-        check_same_device(Q, *V_res, "V_res");
-        check_blob_size(*K_res, cap, bc_sizeof_residual_vec(), "K_res");
-        check_blob_size(*V_res, cap, bc_sizeof_residual_vec(), "V_res");
-        kr = K_res->data_ptr();
-        vr = V_res->data_ptr();
-    }
+    const CachePtrs c = cache_blobs(Q, K_bin, K_res, V_bin, V_res, batch * n_kv_heads * max_seq);
     c10::DeviceGuard guard(Q.device());
     const int64_t seq_len = current_len + 1 < max_seq ? current_len + 1 : max_seq;
     size_t ws_bytes = 0;
@@ -317,8 +335,8 @@ torch::Tensor append_attention(torch::Tensor Q, torch::Tensor k, torch::Tensor v
                  "attention_workspace_size");
     auto ws = workspace_for(Q, ws_bytes);
     auto out = torch::empty({batch, n_heads, head_dim}, Q.options());
-    check_status(bc_append_attention(Q.data_ptr(), k.data_ptr(), v.data_ptr(), K_bin.data_ptr(), kr,
-                                     V_bin.data_ptr(), vr, out.data_ptr(), (int)batch, (int)n_heads,
+    check_status(bc_append_attention(Q.data_ptr(), k.data_ptr(), v.data_ptr(), c.kb, c.kr, c.vb,
+                                     c.vr, out.data_ptr(), (int)batch, (int)n_heads,
                                      (int)n_kv_heads, (int)head_dim, current_len, (int)max_seq,
                                      ws.data_ptr(), ws_bytes, stream_of(Q)),
                  "append_attention");
@@ -332,34 +350,17 @@ torch::Tensor attention_partial(torch::Tensor Q, torch::Tensor K_bin,
                                 int64_t n_kv_heads, int64_t seq_len, int64_t kv_stride,
                                 int64_t head_dim) {
     check_q(Q, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(K_bin);
-    BC_CHECK_BLOB(V_bin);
-    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                "n_heads must be a multiple of n_kv_heads");
-    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
-    const int64_t cap = batch * n_kv_heads * kv_stride;
-    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
-    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
-    TORCH_CHECK(K_res.has_value() == V_res.has_value(), "K_res and V_res: both or neither");
-    void *kr = nullptr, *vr = nullptr;
-    if (K_res.has_value()) {
-        BC_CHECK_BLOB(*K_res);
-        BC_CHECK_BLOB(*V_res);
-        check_blob_size(*K_res, cap, bc_sizeof_residual_vec(), "K_res");
-        check_blob_size(*V_res, cap, bc_sizeof_residual_vec(), "V_res");
-        kr = K_res->data_ptr();
-        vr = V_res->data_ptr();
-    }
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
+    const CachePtrs c = cache_blobs(Q, K_bin, K_res, V_bin, V_res, batch * n_kv_heads * kv_stride);
     c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
                                              (int)seq_len, (int)head_dim, &ws_bytes),
                  "attention_workspace_size");
     auto ws = workspace_for(Q, ws_bytes);
-    check_status(bc_attention_partial(Q.data_ptr(), K_bin.data_ptr(), kr, V_bin.data_ptr(), vr,
-                                      (int)batch, (int)n_heads, (int)n_kv_heads, (int)seq_len,
-                                      (int)kv_stride, (int)head_dim, ws.data_ptr(), ws_bytes,
-                                      stream_of(Q)),
+    check_status(bc_attention_partial(Q.data_ptr(), c.kb, c.kr, c.vb, c.vr, (int)batch,
+                                      (int)n_heads, (int)n_kv_heads, (int)seq_len, (int)kv_stride,
+                                      (int)head_dim, ws.data_ptr(), ws_bytes, stream_of(Q)),
                  "attention_partial");
     return ws;
 }
@@ -382,17 +383,23 @@ torch::Tensor attention_combine(torch::Tensor ws, int64_t batch, int64_t n_heads
     return out;
 }
 
-// Reference signatures (src/torch_binding.cpp:68-117): MHA, blob capacity B*H*S.
+// Reference signatures (src/torch_binding.cpp:68-117): MHA; the stride of the
+// rows comes from the blob's capacity (ref_kv_stride), so the prefix views the
+// reference's BitCache passes read the slots it wrote.
 torch::Tensor binary_attention(torch::Tensor Q, torch::Tensor K_bin, torch::Tensor V_bin,
                                int64_t batch, int64_t n_heads, int64_t seq_len, int64_t head_dim) {
+    const int64_t stride = ref_kv_stride(resolve_blob(K_bin, bc_sizeof_binary_vec(), "K_bin"),
+                                         batch, n_heads, seq_len, "K_bin");
     return attention(Q, K_bin, std::nullopt, V_bin, std::nullopt, batch, n_heads, n_heads, seq_len,
-                     seq_len, head_dim);
+                     stride, head_dim);
 }
 
 torch::Tensor compensated_attention(torch::Tensor Q, torch::Tensor K_bin, torch::Tensor K_res,
                                     torch::Tensor V_bin, torch::Tensor V_res, int64_t batch,
                                     int64_t n_heads, int64_t seq_len, int64_t head_dim) {
-    return attention(Q, K_bin, K_res, V_bin, V_res, batch, n_heads, n_heads, seq_len, seq_len,
+    const int64_t stride = ref_kv_stride(resolve_blob(K_bin, bc_sizeof_binary_vec(), "K_bin"),
+                                         batch, n_heads, seq_len, "K_bin");
+    return attention(Q, K_bin, K_res, V_bin, V_res, batch, n_heads, n_heads, seq_len, stride,
                      head_dim);
 }
 
@@ -401,19 +408,9 @@ std::tuple<torch::Tensor, torch::Tensor> adaptive_attention(
     torch::Tensor V_res, int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t seq_len,
     int64_t kv_stride, int64_t head_dim, int64_t top_k, bool return_selected) {
     check_q(Q, batch, n_heads, head_dim);
-    for (auto* t : {&K_bin, &K_res, &V_bin, &V_res}) {
-        BC_CHECK_BLOB(*t);
-        check_same_device(Q, *t, "cache blob");
-    }
-    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                "n_heads must be a multiple of n_kv_heads");
-    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
     TORCH_CHECK(top_k >= 0, "top_k must be >= 0");
-    const int64_t cap = batch * n_kv_heads * kv_stride;
-    check_blob_size(K_bin, cap, bc_sizeof_binary_vec(), "K_bin");
-    check_blob_size(V_bin, cap, bc_sizeof_binary_vec(), "V_bin");
-    check_blob_size(K_res, cap, bc_sizeof_residual_vec(), "K_res");
-    check_blob_size(V_res, cap, bc_sizeof_residual_vec(), "V_res");
+    const CachePtrs c = cache_blobs(Q, K_bin, K_res, V_bin, V_res, batch * n_kv_heads * kv_stride);
     c10::DeviceGuard guard(Q.device());
     size_t ws_bytes = 0;
     check_status(bc_adaptive_attention_workspace_size((int)batch, (int)n_heads, (int)n_kv_heads,
@@ -428,8 +425,7 @@ std::tuple<torch::Tensor, torch::Tensor> adaptive_attention(
                            torch::TensorOptions().dtype(torch::kUInt8).device(Q.device()));
         selp = sel.data_ptr<uint8_t>();
     }
-    check_status(bc_adaptive_attention(Q.data_ptr(), K_bin.data_ptr(), K_res.data_ptr(),
-                                       V_bin.data_ptr(), V_res.data_ptr(), out.data_ptr(), selp,
+    check_status(bc_adaptive_attention(Q.data_ptr(), c.kb, c.kr, c.vb, c.vr, out.data_ptr(), selp,
                                        (int)batch, (int)n_heads, (int)n_kv_heads, (int)seq_len,
                                        (int)kv_stride, (int)head_dim, (int)top_k, ws.data_ptr(),
                                        ws_bytes, stream_of(Q)),
@@ -442,16 +438,13 @@ std::tuple<torch::Tensor, torch::Tensor> binary_scores(torch::Tensor Q, torch::T
                                                        int64_t n_kv_heads, int64_t seq_len,
                                                        int64_t kv_stride, int64_t head_dim) {
     check_q(Q, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(K_bin);
     check_same_device(Q, K_bin, "K_bin");
-    TORCH_CHECK(n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-                "n_heads must be a multiple of n_kv_heads");
-    TORCH_CHECK(kv_stride >= seq_len, "kv_stride must be >= seq_len");
-    check_blob_size(K_bin, batch * n_kv_heads * kv_stride, bc_sizeof_binary_vec(), "K_bin");
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
+    void* kb = blob_exact(K_bin, batch * n_kv_heads * kv_stride, bc_sizeof_binary_vec(), "K_bin");
     c10::DeviceGuard guard(Q.device());
     auto scores = torch::empty({batch, n_heads, seq_len}, Q.options().dtype(torch::kFloat32));
     auto pcs = torch::empty({batch, n_heads, seq_len}, Q.options().dtype(torch::kInt32));
-    check_status(bc_binary_scores(Q.data_ptr(), K_bin.data_ptr(), scores.data_ptr<float>(),
+    check_status(bc_binary_scores(Q.data_ptr(), kb, scores.data_ptr<float>(),
                                   pcs.data_ptr<int32_t>(), (int)batch, (int)n_heads,
                                   (int)n_kv_heads, (int)seq_len, (int)kv_stride, (int)head_dim,
                                   stream_of(Q)),
@@ -459,19 +452,29 @@ std::tuple<torch::Tensor, torch::Tensor> binary_scores(torch::Tensor Q, torch::T
     return {scores, pcs};
 }
 
-torch::Tensor compute_head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t batch,
-                                   int64_t n_heads, int64_t seq_len, int64_t head_dim) {
+// GQA / ring-stride form (bc_compute_head_entropy_gqa).
+torch::Tensor head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t batch, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t seq_len, int64_t kv_stride,
+                           int64_t head_dim) {
     check_q(Q, batch, n_heads, head_dim);
-    BC_CHECK_BLOB(K_bin);
     check_same_device(Q, K_bin, "K_bin");
-    check_blob_size(K_bin, batch * n_heads * seq_len, bc_sizeof_binary_vec(), "K_bin");
+    check_heads(n_heads, n_kv_heads, seq_len, kv_stride);
+    void* kb = blob_exact(K_bin, batch * n_kv_heads * kv_stride, bc_sizeof_binary_vec(), "K_bin");
     c10::DeviceGuard guard(Q.device());
     auto ent = torch::empty({batch, n_heads}, Q.options().dtype(torch::kFloat32));
-    check_status(bc_compute_head_entropy(Q.data_ptr(), K_bin.data_ptr(), ent.data_ptr<float>(),
-                                         (int)batch, (int)n_heads, (int)seq_len, (int)head_dim,
-                                         stream_of(Q)),
+    check_status(bc_compute_head_entropy_gqa(Q.data_ptr(), kb, ent.data_ptr<float>(), (int)batch,
+                                             (int)n_heads, (int)n_kv_heads, (int)seq_len,
+                                             (int)kv_stride, (int)head_dim, stream_of(Q)),
                  "compute_head_entropy");
     return ent;
+}
+
+// Reference signature (src/torch_binding.cpp:141-162); stride as binary_attention.
+torch::Tensor compute_head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t batch,
+                                   int64_t n_heads, int64_t seq_len, int64_t head_dim) {
+    const int64_t stride = ref_kv_stride(resolve_blob(K_bin, bc_sizeof_binary_vec(), "K_bin"),
+                                         batch, n_heads, seq_len, "K_bin");
+    return head_entropy(Q, K_bin, batch, n_heads, n_heads, seq_len, stride, head_dim);
 }
 
 torch::Tensor adaptive_select(torch::Tensor entropy, double threshold) {
@@ -513,9 +516,11 @@ torch::Tensor reference_attention(torch::Tensor Q, torch::Tensor K, torch::Tenso
 
 // ------------------------------------------------------------------ format conversion
 torch::Tensor convert(torch::Tensor blob, int64_t n, int64_t head_dim, bool residual, bool to_ref) {
-    BC_CHECK_BLOB(blob);
     const int64_t per = residual ? bc_sizeof_residual_vec() : bc_sizeof_binary_vec();
+    BC_CHECK_BLOB(blob);
     TORCH_CHECK(blob.numel() == n * per, "blob must hold n * ", per, " bytes");
+    // a planar input is read at its capacity's plane offsets
+    if (to_ref) blob_exact(blob, n, per, "blob");
     c10::DeviceGuard guard(blob.device());
     auto out = to_ref ? torch::empty({n * per}, blob.options()) : torch::zeros({n * per}, blob.options());
     int st;
@@ -544,6 +549,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("kv"), py::arg("binary_cache"), py::arg("residual_cache"), py::arg("batch"),
           py::arg("n_heads"), py::arg("head_dim"), py::arg("current_len"), py::arg("max_seq"));
     m.def("compute_head_entropy", &compute_head_entropy, "Per-head entropy of binary attention");
+    m.def("head_entropy", &head_entropy, "Per-head entropy, GQA / ring-stride form");
     m.def("sizeof_binary_vec", &sizeof_binary_vec, "Bytes per vector of a binary blob (36)");
     m.def("sizeof_residual_vec", &sizeof_residual_vec, "Bytes per vector of a residual blob (130)");
     // extensions

@@ -107,11 +107,16 @@ def binary_scores(Q: Tensor, K_bin: Tensor, batch: int, n_heads: int, seq_len: i
 
 
 def compute_head_entropy(Q: Tensor, K_bin: Tensor, batch: int, n_heads: int, seq_len: int,
-                         head_dim: int) -> Tensor:
-    """Per-(b,h) entropy of the binary-score softmax (src/adaptive_precision.cu:13-130)."""
+                         head_dim: int, *, n_kv_heads: Optional[int] = None,
+                         kv_stride: Optional[int] = None) -> Tensor:
+    """Per-(b,h) entropy of the binary-score softmax (src/adaptive_precision.cu:13-130),
+    float32 [batch, n_heads].  n_kv_heads / kv_stride: GQA and ring-stride caches."""
     _require_extension()
     _check_q(Q)
-    return _C.compute_head_entropy(Q, K_bin, batch, n_heads, seq_len, head_dim)
+    if n_kv_heads is None and kv_stride is None:
+        return _C.compute_head_entropy(Q, K_bin, batch, n_heads, seq_len, head_dim)
+    return _C.head_entropy(Q, K_bin, batch, n_heads, n_heads if n_kv_heads is None else n_kv_heads,
+                           seq_len, seq_len if kv_stride is None else kv_stride, head_dim)
 
 
 def adaptive_select(entropy: Tensor, threshold: float) -> Tensor:
@@ -135,14 +140,31 @@ def head_mode_attention(Q: Tensor, K_bin: Tensor, K_res: Tensor, V_bin: Tensor, 
 
 def entropy_dispatch_attention(Q: Tensor, K_bin: Tensor, K_res: Tensor, V_bin: Tensor,
                                V_res: Tensor, batch: int, n_heads: int, seq_len: int,
-                               head_dim: int, threshold: float) -> Tuple[Tensor, Tensor]:
-    """The reference's adaptive precision end to end (MHA): per-head entropy of the binary
+                               head_dim: int, threshold: float, *,
+                               n_kv_heads: Optional[int] = None,
+                               kv_stride: Optional[int] = None) -> Tuple[Tensor, Tensor]:
+    """The reference's adaptive precision end to end: per-head entropy of the binary
     scores (src/adaptive_precision.cu:13-130), mode = binary where entropy >= threshold
     (:133-144), then head_mode_attention.  Returns (out, modes)."""
-    ent = compute_head_entropy(Q, K_bin, batch, n_heads, seq_len, head_dim)
+    kw = dict(n_kv_heads=n_kv_heads, kv_stride=kv_stride)
+    ent = compute_head_entropy(Q, K_bin, batch, n_heads, seq_len, head_dim, **kw)
     modes = adaptive_select(ent, threshold).view(batch, n_heads)
-    return head_mode_attention(Q, K_bin, K_res, V_bin, V_res, modes, batch, n_heads, seq_len,
-                               head_dim), modes
+    hkv = n_heads if n_kv_heads is None else n_kv_heads
+    if kv_stride is None:
+        # the stride compute_head_entropy read with: the blob's capacity per kv row
+        # (a prefix view of a ring reads the ring's own stride)
+        kv_stride = _capacity(K_bin, _C.sizeof_binary_vec()) // max(batch * hkv, 1)
+    out = head_mode_attention(Q, K_bin, K_res, V_bin, V_res, modes, batch, n_heads, seq_len,
+                              head_dim, n_kv_heads=hkv, kv_stride=kv_stride)
+    return out, modes
+
+
+def _capacity(blob: Tensor, per: int) -> int:
+    """Vectors a blob was laid out for: its storage's when it is a prefix view
+    of a larger allocation, else its own (the operators' rule)."""
+    stor = blob.untyped_storage().nbytes()
+    prefix = blob.storage_offset() == 0 and blob.numel() < stor
+    return (stor if prefix else blob.numel()) // per
 
 
 def reference_attention(Q: Tensor, K: Tensor, V: Tensor, batch: int, n_heads: int, seq_len: int,

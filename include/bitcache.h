@@ -189,6 +189,15 @@ int bc_binary_scores(const void* q, const void* k_bin, float* scores, int32_t* p
 int bc_compute_head_entropy(const void* q, const void* k_bin, float* entropy, int batch,
                             int n_heads, int seq_len, int head_dim, void* stream);
 
+/* General form of bc_compute_head_entropy: GQA (query head h reads kv head
+ * h / (n_heads / n_kv_heads)) and a ring-buffer stride (blob capacity
+ * batch*n_kv_heads*kv_stride, keys [0, seq_len) valid), so that the entropy of
+ * a partly filled ring cache can be taken.  No counterpart in the reference
+ * (which assumes n_kv_heads == n_heads and kv_stride == seq_len). */
+int bc_compute_head_entropy_gqa(const void* q, const void* k_bin, float* entropy, int batch,
+                                int n_heads, int n_kv_heads, int seq_len, int kv_stride,
+                                int head_dim, void* stream);
+
 /* mode[i] = entropy[i] >= threshold ? 0 (binary) : 1 (compensated).
  * Replaces launch_adaptive_select (src/adaptive_precision.cu:171-186). */
 int bc_adaptive_select(const float* entropy, uint8_t* modes, int batch, int n_heads,

@@ -66,3 +66,30 @@ def close(got: np.ndarray, ref: np.ndarray, rel=REL_TOL, cos=COS_TOL, what=""):
     assert err <= rel, f"max-abs rel err {err:.3e} > {rel} {what}"
     assert c >= cos, f"cosine {c:.6f} < {cos} {what}"
     return err, c
+
+
+def ring_oracle_attend(q, hist_k, hist_v, max_seq, B, Hq, Hkv, d, compensated=True):
+    """Oracle attention over the tokens a ring of max_seq slots per row holds
+    after appending hist_k / hist_v ([B, Hkv, d] per step, online-encode math):
+    the last min(len, max_seq) tokens (slot order does not matter for softmax
+    attention).  Returns the fp32 output [B, Hq, d]."""
+    n = min(len(hist_k), max_seq)
+    slots = {}
+    for t, (k, v) in enumerate(zip(hist_k, hist_v)):
+        slots[t % max_seq] = (k, v)
+    ks = np.stack([slots[s][0] for s in range(n)], axis=2)  # [B, Hkv, n, d]
+    vs = np.stack([slots[s][1] for s in range(n)], axis=2)
+    Kb, Kr = O.online_encode(ks.reshape(-1, d))
+    Vb, Vr = O.online_encode(vs.reshape(-1, d))
+    if compensated:
+        return O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, n, n_kv_heads=Hkv,
+                                       return_f32=True)[1]
+    return O.binary_attention(q, Kb, Vb, B, Hq, n, n_kv_heads=Hkv, return_f32=True)[1]
+
+
+def ring_oracle_keys(hist_k, max_seq, B, Hkv, d):
+    """Online-encoded K of the tokens a ring holds (as ring_oracle_attend)."""
+    n = min(len(hist_k), max_seq)
+    slots = {t % max_seq: k for t, k in enumerate(hist_k)}
+    ks = np.stack([slots[s] for s in range(n)], axis=2)
+    return O.online_encode(ks.reshape(-1, d))[0], n

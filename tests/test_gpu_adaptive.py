@@ -45,6 +45,17 @@ CASES = [
     # passes over key chunks of 1024 (several per head), without and with ties
     (16, 32, 8, 8192, 128, 820, False),
     (16, 32, 8, 8192, 128, 820, True),
+    # head dims without the matrix-core kernel (the VALU split kernel's
+    # adaptive mode), MHA and GQA
+    (1, 2, 2, 300, 32, 30, False),
+    (1, 8, 2, 520, 32, 52, True),
+    (1, 4, 4, 900, 96, 90, False),
+    (1, 8, 2, 700, 96, 70, False),
+    (1, 4, 4, 600, 160, 60, True),
+    (1, 8, 2, 500, 160, 50, False),
+    (1, 4, 2, 400, 192, 40, False),
+    (1, 2, 2, 350, 224, 35, False),
+    (1, 8, 4, 333, 224, 34, True),
 ]
 
 

@@ -6,25 +6,9 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.gpu_util import close, say, slice_enc, to_np
+from tests.gpu_util import close, ring_oracle_attend, say, slice_enc, to_np
 
 pytestmark = pytest.mark.gpu
-
-
-def oracle_attend(q, hist_k, hist_v, ring: O.RingState, B, Hq, Hkv, d, compensated=True):
-    """Attention over the tokens currently in the ring (slot order does not
-    matter for softmax attention)."""
-    n = ring.filled
-    slots = {}
-    for t, (k, v) in enumerate(zip(hist_k, hist_v)):
-        slots[t % ring.max_seq] = (k, v)
-    ks = np.stack([slots[s][0] for s in range(n)], axis=2)  # [B, Hkv, n, d]
-    vs = np.stack([slots[s][1] for s in range(n)], axis=2)
-    Kb, Kr = O.online_encode(ks.reshape(-1, d))
-    Vb, Vr = O.online_encode(vs.reshape(-1, d))
-    if compensated:
-        return O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, n, n_kv_heads=Hkv, return_f32=True)[1]
-    return O.binary_attention(q, Kb, Vb, B, Hq, n, n_kv_heads=Hkv, return_f32=True)[1]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,d,max_seq,steps,comp", [
@@ -50,7 +34,7 @@ def test_bitcache_append_attend(B, Hq, Hkv, d, max_seq, steps, comp):
         if t in (0, steps // 2, steps - 1):
             q = (rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)
             out = cache.attend(torch.from_numpy(q).cuda())
-            ref = oracle_attend(q, hk, hv, ring, B, Hq, Hkv, d, comp)
+            ref = ring_oracle_attend(q, hk, hv, max_seq, B, Hq, Hkv, d, comp)
             close(to_np(out).astype(np.float32), ref, what=f"step {t}")
     assert cache.seq_len == ring.filled
     if not comp:
