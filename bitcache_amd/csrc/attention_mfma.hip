@@ -71,16 +71,33 @@ __device__ __forceinline__ SignWords<D> buf_signs(__amdgpu_buffer_rsrc_t r, int 
     return s;
 }
 
+// The query of the INT4 residual dot as 24-bit fixed point:
+// q_int = rint(q / step), step = max|q| / kQIntMax, written as six balanced
+// int4 digits (q_int = sum_j d_j 16^j, d_j in [-8, 7]) or three balanced int8
+// planes (q_int = p0 + 256 p1 + 65536 p2).  A tile's dots use the top 16 bits
+// (digits 2..5, planes 1..2: q_int / 256 within 0.53, i.e. 16-bit fixed point
+// of step 256*step) unless a key of the tile could see a score error above
+// kPrecNats from it; then the low digits / plane are added (an fp32-level
+// error).  kQIntMax leaves room below 7*(16^6 - 1)/15 = 7829367, the largest
+// six-digit value, for the rounding of q / step.
+constexpr float kQIntMax = 7800000.0f;
+constexpr float kPrecNats = 1.0f / 2048.0f;
+
 template <int D, int G>
 struct QDigits {
     uint32_t signs[G][D / 32];
-    int4 digits[G][D / 8];        // .x..w = balanced int4 digits 0..3 of elements 8w..8w+7 (nibble k = element 8w+k)
-    int16_t qint[G][D];           // q_int = rint(q / dq), |q_int| <= 30583
+    int4 digits[G][D / 8];        // .x..w = balanced int4 digits 2..5 of q_int of elements 8w..8w+7 (nibble k = element 8w+k)
+    int2 digits_lo[G][D / 8];     // digits 0..1
     // int8 MFMA B operands of the K residual dot (GQA groups, d >= 128):
-    // [piece][half][lane] (see the kernel)
+    // [piece][half][lane] (see the kernel): planes 1, 2 (and plane 0 where
+    // the columns hold it), and plane 0 for groups of more than 5 heads
     int4 bq[(G > 1 && D >= 128) ? D / 128 : 1][2][(G > 1 && D >= 128) ? 64 : 1];
+    int4 bq_lo[(G > 5 && D >= 128) ? D / 128 : 1][2][(G > 5 && D >= 128) ? 64 : 1];
     float scale_q[G];             // sequential mean |q| (src/compensated_attention.cu:65-67)
-    float dq[G];                  // fixed-point step of q_int
+    float dq[G];                  // step of the top 16 bits: 256 * step of q_int
+    // bound on a key's score error (nats) from the top-16-bit dot, per unit of
+    // its residual scale: 0.53 * max_g dq * D / sqrt(D)
+    float prec_bound;
 };
 
 // Per-wave LDS, one __shared__ array per role (the compiler tracks LDS
@@ -119,6 +136,13 @@ struct KRegs {
     uint32_t sel;                 // adaptive: bit g = head g selected the lane's key
 };
 
+// Eight INT4 codes of two dwords as the int8 MFMA operand 16*n (signed): low
+// nibbles shifted up, high nibbles masked in place.
+__device__ __forceinline__ v4i_t codes_i8(uint32_t x0, uint32_t x1) {
+    return v4i_t{(int)((x0 << 4) & 0xF0F0F0F0u), (int)(x0 & 0xF0F0F0F0u), (int)((x1 << 4) & 0xF0F0F0F0u),
+                 (int)(x1 & 0xF0F0F0F0u)};
+}
+
 // x through an empty asm: the compiler cannot split or re-associate it
 __device__ __forceinline__ int opaque_int(int x) {
     asm volatile("" : "+v"(x));
@@ -147,9 +171,10 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
 
 // Query preparation of one workgroup (256 threads), spread over all threads:
 // the query as floats and its sign words (a wave ballot per 64 elements);
-// scale_q (sequential fp32 order, element 0 first) and the fixed-point step dq
-// per head; q_int = rint(q / dq) per element; then the balanced int4 digit
-// words (one (word, digit) pair per thread) and the int8 MFMA operand words.
+// scale_q (sequential fp32 order, element 0 first) and the fixed-point step
+// per head; q_int = rint(q / step) per element (in place of the floats); then
+// the balanced int4 digit words (one (word, digit) pair per thread) and the
+// int8 MFMA operand words.
 template <int D, int G, bool KMF>
 __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf) {
     static_assert((G * D) % 64 == 0, "whole waves of query elements");
@@ -176,59 +201,80 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
             mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         qd.scale_q[tid] = acc / (float)D;
-        // |q_int| <= 30583 keeps the top digit in [-8, 7]
-        qd.dq[tid] = mx > 0.0f ? mx / 30583.0f : 1.0f;
+        qd.dq[tid] = mx > 0.0f ? 256.0f * (mx / kQIntMax) : 256.0f;
     }
     __syncthreads();
-    for (int i = tid; i < G * D; i += 256) {
-        const int g = i / D;
-        qd.qint[g][i % D] = (int16_t)(int)__builtin_rintf(qf[i] / qd.dq[g]);
+    if (tid == 0) {
+        float m = 0.0f;
+        for (int g = 0; g < G; g++) m = fmaxf(m, qd.dq[g]);
+        qd.prec_bound = 0.53f * m * sqrtf((float)D);
     }
+    // q_int over the floats: each thread converts the elements it reads
+    int* qint = (int*)qf;
+    for (int i = tid; i < G * D; i += 256)
+        qint[i] = (int)__builtin_rintf(qf[i] / (qd.dq[i / D] * (1.0f / 256.0f)));
     __syncthreads();
     // digit j of the 8 elements of word w: nibble k = element 8w + k (balanced
     // base 16: t = sum_j d_j 16^j, d_j in [-8, 7])
-    for (int e = tid; e < G * (D / 8) * 4; e += 256) {
-        const int j = e & 3, gw = e >> 2, g = gw / (D / 8), w = gw % (D / 8);
+    for (int e = tid; e < G * (D / 8) * 6; e += 256) {
+        const int j = e % 6, gw = e / 6, g = gw / (D / 8), w = gw % (D / 8);
         uint32_t word = 0u;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            int t = qd.qint[g][8 * w + k];
+            int t = qint[g * D + 8 * w + k];
             int d = 0;
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
+            for (int jj = 0; jj < 6; jj++) {
                 d = ((t + 8) & 15) - 8;
                 if (jj == j) break;
                 t = (t - d) >> 4;
             }
             word |= ((uint32_t)d & 0xFu) << (4 * k);
         }
-        ((int*)&qd.digits[g][w])[j] = (int)word;
+        if (j >= 2) ((int*)&qd.digits[g][w])[j - 2] = (int)word;
+        else ((int*)&qd.digits_lo[g][w])[j] = (int)word;
     }
     if constexpr (KMF) {
-        // B operand words: column c = 2g + p is digit plane p of head g
-        // (q_int = d0 + 256 d1, d0 in [-128, 127]); slot s = 4r + j of lane
-        // group q for piece pc and half h holds dim
-        // 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the unpacked codes put it
+        // B operand words, q_int = p0 + 256 p1 + 65536 p2 with p_i in
+        // [-128, 127]: column c = 2g + p (c < 2G) holds plane p + 1 of head g,
+        // column 2G + g plane 0 of head g when 3G <= 16 (bq_lo column 2g
+        // otherwise); slot s = 4r + j of lane group q for piece pc and half h
+        // holds dim 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the unpacked
+        // codes put it
         constexpr int NPC = D / 128;
+        constexpr bool LO_COLS = 3 * G <= 16;
         for (int e = tid; e < NPC * 2 * 64; e += 256) {
             const int pc = e / 128, h = (e / 64) & 1, ln = e & 63;
-            const int col = ln & 15, qg4 = ln >> 4, gh = col >> 1, pl = col & 1;
-            int wd[4];
+            const int col = ln & 15, qg4 = ln >> 4;
+            int wd[4], wl[4];
             for (int r = 0; r < 4; r++) {
-                uint32_t word = 0;
+                uint32_t word = 0, wlo = 0;
                 for (int j = 0; j < 4; j++) {
                     const int dim = 32 * (qg4 + 4 * pc) + 8 * (2 * h + (r >> 1)) + 2 * j + (r & 1);
-                    int v = 0;
-                    if (gh < G) {
-                        const int t = qd.qint[gh][dim];
-                        const int d0 = ((t + 128) & 255) - 128;
-                        v = pl == 0 ? d0 : (t - d0) >> 8;
+                    auto planes = [&](int g, int& p0, int& p1, int& p2) {
+                        const int t = qint[g * D + dim];
+                        p0 = ((t + 128) & 255) - 128;
+                        const int t1 = (t - p0) >> 8;
+                        p1 = ((t1 + 128) & 255) - 128;
+                        p2 = (t1 - p1) >> 8;
+                    };
+                    int p0, p1, p2, v = 0, vl = 0;
+                    if (col < 2 * G) {
+                        planes(col >> 1, p0, p1, p2);
+                        v = (col & 1) ? p2 : p1;
+                        if (!LO_COLS && !(col & 1)) vl = p0;
+                    } else if (LO_COLS && col < 3 * G) {
+                        planes(col - 2 * G, p0, p1, p2);
+                        v = p0;
                     }
                     word |= ((uint32_t)v & 0xFFu) << (8 * j);
+                    wlo |= ((uint32_t)vl & 0xFFu) << (8 * j);
                 }
                 wd[r] = (int)word;
+                wl[r] = (int)wlo;
             }
             qd.bq[pc][h][ln] = make_int4(wd[0], wd[1], wd[2], wd[3]);
+            if constexpr (!LO_COLS) qd.bq_lo[pc][h][ln] = make_int4(wl[0], wl[1], wl[2], wl[3]);
         }
     }
     __syncthreads();
@@ -342,6 +388,7 @@ void attn_mfma_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds_st1[4][PIPE ? WL::kStage : 16];
     __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][WL::kWeightBytes / 2];
     __shared__ __attribute__((aligned(16))) int lds_rd[4][WL::kRdInts];
+    __shared__ __attribute__((aligned(16))) int lds_rdlo[4][(KMF && 3 * G <= 16) ? WL::kRdInts : 1];
     __shared__ float wofs[4][G];
     __shared__ float wm[4][G], wlsum[4][G], wsc[4];
 
@@ -413,6 +460,7 @@ void attn_mfma_kernel(AttnArgs a) {
     uint16_t* wsl = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + slot_of(kown));
     const uint16_t* wrd = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + bcol * WL::kColSlots + 16 * g4);
     int* rdl = lds_rd[wave];          // [64 keys][G] residual dots
+    int* rdlo = lds_rdlo[wave];       // their plane-0 parts (precise tiles)
 
     // softmax reference per head, lowered lazily: weights p = 2^(s - m) stay
     // <= 2^kTau, and the accumulators are rescaled only when a score passes
@@ -739,10 +787,15 @@ void attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        // residual dot on the raw int4 codes: sum_i q_int_i * n_i per head
+        // residual dot on the raw int4 codes: sum_i q_int_i * n_i per head, in
+        // units of the top-16-bit step dq (racc, exact integers; in a precise
+        // tile the float bits of that plus the low digits' part / 256)
         int racc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) racc[g] = 0;
+        // precise tile: some key's score could move by more than kPrecNats
+        // from the top 16 bits alone (uniform over the wave)
+        const bool prec = RES && __ballot(rsk * qd.prec_bound > kPrecNats) != 0ull;
         if constexpr (KMF) {
           // key blocks holding codes: all four, or (adaptive) the blocks of
           // the nsel compacted positions
@@ -752,31 +805,48 @@ void attn_mfma_kernel(AttnArgs a) {
             // place; each half of a piece is one 16x16x64 MFMA of (head, digit
             // plane) rows x 64 dims times 64 dims x 16 keys (columns of keys whose
             // codes were not loaded are never used)
+            // Lane l holds rows 4(l/16) + i = (head 2(l/16) + i/2, plane i%2 + 1)
+            // of position 16kb + l%16: both planes of a head sit in one lane, and
+            // q_int dot * 16 / 256 = plane1 + 256 plane2 goes to rdl[position][head].
+            // Plane 0 of a precise tile (q_int dot * 16 = 65536 plane2 +
+            // 256 plane1 + plane0): groups of more than 5 heads take it from a
+            // second B operand (LDS) into the same lanes and store the float
+            // bits of the sum; smaller groups have it in rows 2G + g (below)
+            constexpr bool LO_COLS = 3 * G <= 16;
             v4i_t acc[4];
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
                 if (kb >= nkb) break;
                 acc[kb] = v4i_t{0, 0, 0, 0};
+                v4i_t accl = v4i_t{0, 0, 0, 0};
 #pragma unroll
                 for (int pc = 0; pc < NPC; pc++)
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
-                        const uint32_t x0 = kc[4 * (kb * NPC + pc) + 2 * h];
-                        const uint32_t x1 = kc[4 * (kb * NPC + pc) + 2 * h + 1];
-                        const v4i_t av = v4i_t{(int)((x0 << 4) & 0xF0F0F0F0u), (int)(x0 & 0xF0F0F0F0u),
-                                               (int)((x1 << 4) & 0xF0F0F0F0u), (int)(x1 & 0xF0F0F0F0u)};
+                        const v4i_t av = codes_i8(kc[4 * (kb * NPC + pc) + 2 * h], kc[4 * (kb * NPC + pc) + 2 * h + 1]);
                         acc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bq[pc][h], av, acc[kb], 0, 0, 0);
+                        if (!LO_COLS && prec) {
+                            const int4 w = qd.bq_lo[pc][h][lane];
+                            accl = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i_t{w.x, w.y, w.z, w.w}, av, accl, 0, 0, 0);
+                        }
                     }
+                if (lane < 8 * G) {
+                    int2 v = make_int2(acc[kb][0] + 256 * acc[kb][1], acc[kb][2] + 256 * acc[kb][3]);
+                    if (!LO_COLS && prec)
+                        v = make_int2(__builtin_bit_cast(int, (float)v.x + (float)accl[0] * (1.0f / 256.0f)),
+                                      __builtin_bit_cast(int, (float)v.y + (float)accl[2] * (1.0f / 256.0f)));
+                    *(int2*)&rdl[(16 * kb + lj) * G + 2 * g4] = v;
+                }
             }
-            // lane l holds rows 4(l/16) + i = (head 2(l/16) + i/2, plane i%2) of
-            // position 16kb + l%16: both planes of a head sit in one lane, and
-            // q_int dot * 16 = plane0 + 256 plane1 goes to rdl[position][head]
-            if (lane < 8 * G) {
+            if (LO_COLS && prec && g4 == G / 2) {
+                // plane 0 (q_int dot * 16 = 65536 plane2 + 256 plane1 + plane0)
+                // to rdlo[position][head]: rows 2G + g of the same MFMAs (lane
+                // group G/2, i = g)
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++) {
                     if (kb >= nkb) break;
-                    *(int2*)&rdl[(16 * kb + lj) * G + 2 * g4] =
-                        make_int2(acc[kb][0] + 256 * acc[kb][1], acc[kb][2] + 256 * acc[kb][3]);
+#pragma unroll
+                    for (int g = 0; g < (LO_COLS ? G : 1); g++) rdlo[(16 * kb + lj) * G + g] = acc[kb][g];
                 }
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -793,6 +863,11 @@ void attn_mfma_kernel(AttnArgs a) {
             } else {
 #pragma unroll
                 for (int g = 0; g < G; g++) racc[g] = rdl[rpos * G + g];
+            }
+            if (LO_COLS && prec) {
+#pragma unroll
+                for (int g = 0; g < G; g++)
+                    racc[g] = __builtin_bit_cast(int, (float)racc[g] + (float)rdlo[rpos * G + g] * (1.0f / 256.0f));
             }
           }
         } else if constexpr (LIN_K) {
@@ -815,10 +890,44 @@ void attn_mfma_kernel(AttnArgs a) {
                         s2 = __builtin_amdgcn_sdot8(dg.z, x, s2, false);
                         s3 = __builtin_amdgcn_sdot8(dg.w, x, s3, false);
                     }
-                    const int tot = row_group_sum<Q>(s0 + 16 * s1 + 256 * s2 + 4096 * s3);
+                    int tot = row_group_sum<Q>(s0 + 16 * s1 + 256 * s2 + 4096 * s3);
+                    if (G > 1 && prec) {
+                        // digits 0..1: the dot becomes tot + lo / 256 (float bits)
+                        int l0 = 0, l1 = 0;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int2 dl = qd.digits_lo[g][4 * quarter + j + z];
+                            const int x = (int)kc[4 * i + j];
+                            l0 = __builtin_amdgcn_sdot8(dl.x, x, l0, false);
+                            l1 = __builtin_amdgcn_sdot8(dl.y, x, l1, false);
+                        }
+                        const int totl = row_group_sum<Q>(l0 + 16 * l1);
+                        tot = __builtin_bit_cast(int, (float)tot + (float)totl * (1.0f / 256.0f));
+                    }
                     racc[g] = quarter == i ? tot : racc[g];
                 }
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            if (G == 1 && prec) {
+                // (a single head: a separate pass keeps the register peak of
+                // the main loop) digits 0..1: the dot becomes racc + lo / 256
+#pragma unroll
+                for (int i = 0; i < Q; i++) {
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        int l0 = 0, l1 = 0;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int2 dl = qd.digits_lo[g][4 * quarter + j + z];
+                            const int x = (int)kc[4 * i + j];
+                            l0 = __builtin_amdgcn_sdot8(dl.x, x, l0, false);
+                            l1 = __builtin_amdgcn_sdot8(dl.y, x, l1, false);
+                        }
+                        const int totl = row_group_sum<Q>(l0 + 16 * l1);
+                        if (quarter == i)
+                            racc[g] = __builtin_bit_cast(int, (float)racc[g] + (float)totl * (1.0f / 256.0f));
+                    }
+                }
             }
         } else if constexpr (G == 1 && RES && !LIN_K) {
             {
@@ -831,6 +940,16 @@ void attn_mfma_kernel(AttnArgs a) {
                     s3 = __builtin_amdgcn_sdot8(sdig[w][3], (int)kc[w], s3, false);
                 }
                 racc[0] = s0 + 16 * s1 + 256 * s2 + 4096 * s3;
+                if (prec) {
+                    int l0 = 0, l1 = 0;
+#pragma unroll
+                    for (int w = 0; w < CW; w++) {
+                        const int2 dl = qd.digits_lo[0][w];
+                        l0 = __builtin_amdgcn_sdot8(dl.x, (int)kc[w], l0, false);
+                        l1 = __builtin_amdgcn_sdot8(dl.y, (int)kc[w], l1, false);
+                    }
+                    racc[0] = __builtin_bit_cast(int, (float)racc[0] + (float)(l0 + 16 * l1) * (1.0f / 256.0f));
+                }
             }
         } else if constexpr (RES) {
             bool any_res = ALLRES;
@@ -856,6 +975,19 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
                 for (int g = 0; g < G; g++)
                     racc[g] = sa[g][0] + 16 * sa[g][1] + 256 * sa[g][2] + 4096 * sa[g][3];
+                if (prec) {
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        int l0 = 0, l1 = 0;
+#pragma unroll
+                        for (int w = 0; w < CW; w++) {
+                            const int2 dl = qd.digits_lo[g][w + z];
+                            l0 = __builtin_amdgcn_sdot8(dl.x, (int)kc[w], l0, false);
+                            l1 = __builtin_amdgcn_sdot8(dl.y, (int)kc[w], l1, false);
+                        }
+                        racc[g] = __builtin_bit_cast(int, (float)racc[g] + (float)(l0 + 16 * l1) * (1.0f / 256.0f));
+                    }
+                }
             }
         }
         float sc[G];
@@ -865,9 +997,11 @@ void attn_mfma_kernel(AttnArgs a) {
             bool use_res = MODE == MODE_COMP;
             if constexpr (MODE == MODE_ADAPTIVE) use_res = (selmask >> g) & 1u;
             if constexpr (MODE == MODE_MIXED) use_res = hmode[g];
-            // (the matrix-core dots come x16, an exact power of two)
+            // the dot in units of dq (the matrix-core dots come x16, an exact
+            // power of two; in a precise tile they are float bits already)
+            const float rd = prec ? __builtin_bit_cast(float, racc[g]) : (float)racc[g];
             if (RES && use_res)
-                score = score + (float)racc[g] * (qd.dq[g] * (rsk * (KMF ? 1.0f / 112.0f : 1.0f / 7.0f)));
+                score = score + rd * (qd.dq[g] * (rsk * (KMF ? 1.0f / 112.0f : 1.0f / 7.0f)));
             sc[g] = valid ? score * isd2 : -INFINITY;
         }
 
