@@ -95,3 +95,28 @@ def make_c2(cfg: Config = CONFIGS["c2"], device="cuda", seq_len=None):
 def algorithmic_bytes_per_key(d=D, residual=True):
     """Bytes of one K or V vector that attention must read: d/8 + 2 (+ d/2 + 2)."""
     return d // 8 + 2 + ((d // 2 + 2) if residual else 0)
+
+
+def kendall_tau_ab(x, y):
+    """Kendall tau-a and tau-b of two score vectors (numpy, one head), in
+    O(n log n).  tau-a = (C - D) / (n (n - 1) / 2) with tied pairs counted as
+    neither concordant nor discordant: the reference's own statistic
+    (tests/test_correctness.cu:58-71); tau-b divides C - D by
+    sqrt((n0 - n1)(n0 - n2)) instead (n1, n2: pairs tied in x, in y)."""
+    import numpy as np
+    from scipy.stats import kendalltau
+
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    n = x.size
+    n0 = n * (n - 1) / 2.0
+    if n0 == 0:
+        return 1.0, 1.0
+
+    def tied_pairs(a):
+        _, c = np.unique(a, return_counts=True)
+        return float((c * (c - 1) / 2.0).sum())
+
+    tb = float(kendalltau(x, y).statistic)
+    cd = tb * np.sqrt((n0 - tied_pairs(x)) * (n0 - tied_pairs(y)))
+    return float(cd / n0), tb

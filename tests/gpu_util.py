@@ -93,3 +93,21 @@ def ring_oracle_keys(hist_k, max_seq, B, Hkv, d):
     slots = {t % max_seq: k for t, k in enumerate(hist_k)}
     ks = np.stack([slots[s] for s in range(n)], axis=2)
     return O.online_encode(ks.reshape(-1, d))[0], n
+
+
+def blob_head_tensors(kb, kr, vb, vr, n, d, lo, S):
+    """One (b, head)'s S keys starting at cache vector lo, read from the
+    device blobs (capacity n) as the torch-CPU tensors
+    oracle.compensated_attention_torch_cpu takes: sign words (int64 view of
+    the u32 words), fp16 scales, int8 codes, fp16 residual scales, for K then V."""
+    def planes(bb, rb):
+        w = bb[lo * d // 8:(lo + S) * d // 8].cpu().view(torch.int32).view(S, d // 32)
+        sc = bb[n * d // 8 + 2 * lo:n * d // 8 + 2 * (lo + S)].cpu().view(torch.float16)
+        c = rb[lo * d // 2:(lo + S) * d // 2].cpu().view(S, d // 2).to(torch.int16)
+        lo_, hi_ = c & 0xF, (c >> 4) & 0xF
+        lo_ = torch.where(lo_ >= 8, lo_ - 16, lo_)
+        hi_ = torch.where(hi_ >= 8, hi_ - 16, hi_)
+        codes = torch.stack([lo_, hi_], dim=-1).reshape(S, d).to(torch.int8)
+        rs = rb[n * d // 2 + 2 * lo:n * d // 2 + 2 * (lo + S)].cpu().view(torch.float16)
+        return w.to(torch.int64) & 0xFFFFFFFF, sc, codes, rs
+    return planes(kb, kr) + planes(vb, vr)

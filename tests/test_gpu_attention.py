@@ -9,7 +9,8 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.gpu_util import bin_from_blob, close, res_from_blob, say, slice_enc, to_np
+from tests.gpu_util import (assert_same_bin, assert_same_res, bin_from_blob, blob_head_tensors, close,
+                            res_from_blob, say, slice_enc, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -194,17 +195,24 @@ def test_config_c2_full_size_scores(F):
         qh = to_np(q[b, h])[None, None]
         esc = O.binary_scores(qh, Kh, 1, 1, S)
         assert np.array_equal(to_np(sc[b, h]).view(np.uint32), esc[0, 0].view(np.uint32))
-    # Kendall tau-b of binary scores vs exact q.k on one head (reported, not gated)
-    from scipy.stats import kendalltau
-    exact = (k[0, 0].float() @ q[0, 0].float()).cpu().numpy()
-    tau = kendalltau(to_np(sc[0, 0]), exact).statistic
-    say(f"c2 Kendall tau-b (binary vs exact, head 0): {tau:.4f}")
-    assert tau > 0.2
+    # Kendall tau-a (the reference's statistic, tests/test_correctness.cu:58-71)
+    # and tau-b of the binary scores against exact q.k over all 256 heads
+    # (reported; the README's "> 0.95" is not a gate)
+    exact = torch.matmul(k.float(), q.float().unsqueeze(-1)).squeeze(-1).cpu().numpy()
+    scn = to_np(sc)
+    taus = np.array([W.kendall_tau_ab(scn[b, h], exact[b, h]) for b in range(B) for h in range(H)])
+    say(f"c2 Kendall tau over {len(taus)} heads: tau-a mean {taus[:, 0].mean():.4f} "
+        f"min {taus[:, 0].min():.4f}; tau-b mean {taus[:, 1].mean():.4f} min {taus[:, 1].min():.4f}")
+    assert taus[:, 1].min() > 0.2 and np.all(taus[:, 0] <= taus[:, 1] + 1e-12)
 
 
 def test_config_c3_full_size(F):
-    """Config c3 at full size (B8 H32 S65536): two (b,h) heads against the
-    oracle; every head against the exact fp16 attention as a quality report."""
+    """Config c3 at full size (B8 H32 S65536): every one of the 256 (b, h)
+    heads against the torch-CPU restatement of the reference algorithm on the
+    same device blobs, at the north_star tolerance (max-abs error relative to
+    max |ref| <= 2e-3 over the step, cosine >= 0.9999 per head); the encoded
+    bytes of two heads against the oracle's encoders; and every head against
+    the exact fp16 attention as a quality report."""
     from bitcache_amd import workloads as W
     cfg = W.CONFIGS["c3"]
     say("case c3 full size")
@@ -214,18 +222,70 @@ def test_config_c3_full_size(F):
     vb, vr = F.encode_fused(v.view(-1, d))
     out = F.compensated_attention(q, kb, kr, vb, vr, B, H, S, d)
     torch.cuda.synchronize()
+    n = B * H * S
     for (b, h) in [(0, 0), (5, 17)]:
-        kh = to_np(k[b, h])
-        vh = to_np(v[b, h])
-        Kb, Kr = O.encode_fused(kh)
-        Vb, Vr = O.encode_fused(vh)
-        _, ref = O.compensated_attention(to_np(q[b, h])[None, None], Kb, Kr, Vb, Vr, 1, 1, S,
-                                         return_f32=True)
-        close(to_np(out[b, h]).astype(np.float32), ref[0, 0], what=f"c3 head {(b, h)}")
+        lo = (b * H + h) * S
+        Kb, Kr = O.encode_fused(to_np(k[b, h]))
+        assert_same_bin(slice_enc(bin_from_blob(kb, n, d), lo, lo + S), Kb, f"c3 head {(b, h)}")
+        assert_same_res(slice_enc(res_from_blob(kr, n, d), lo, lo + S), Kr, f"c3 head {(b, h)}")
+    torch.set_num_threads(min(16, len(__import__("os").sched_getaffinity(0))))
+    ref = np.empty((B, H, d), np.float32)
+    got = to_np(out).astype(np.float32)
+    qc = q.cpu()
+    for b in range(B):
+        for h in range(H):
+            args = blob_head_tensors(kb, kr, vb, vr, n, d, (b * H + h) * S, S)
+            ref[b, h] = O.compensated_attention_torch_cpu(qc[b, h], *args).float().numpy()
+        say(f"  c3 batch {b}: heads checked")
+    close(got, ref, what="c3 all heads")
+    cosh = (got * ref).sum(-1) / (np.linalg.norm(got, axis=-1) * np.linalg.norm(ref, axis=-1))
+    say(f"c3 all 256 heads vs torch-CPU restatement: min cosine {cosh.min():.7f}")
+    assert cosh.min() >= 0.9999
     exact = F.reference_attention(q, k, v, B, H, S, d).float()
     cos = torch.nn.functional.cosine_similarity(out.float().view(-1, d), exact.view(-1, d), dim=1)
     say(f"c3 compensated vs exact fp16 attention: mean cos {cos.mean().item():.5f} "
         f"min {cos.min().item():.5f}")
+    assert cos.mean().item() > 0.9
+
+
+def test_config_c1(F):
+    """Config c1 on its own inputs (W.make_qkv: B1 H32 S4096, N(0, 1/128),
+    seed 0) through the reference's two-step path (encode, compute_residual,
+    compensated_attention): bytes against the oracle's encoders, output
+    against the oracle at the north_star tolerance, and against fp16
+    reference attention (the reference checks cosine and max-abs error
+    there; reported, cosine gated at > 0.9)."""
+    from bitcache_amd import workloads as W
+    cfg = W.CONFIGS["c1"]
+    say("case c1")
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, v = W.make_qkv(cfg)
+    kf, vf = k.view(-1, d), v.view(-1, d)
+    kb = F.encode(kf)
+    kr = F.compute_residual(kf, kb)
+    vb = F.encode(vf)
+    vr = F.compute_residual(vf, vb)
+    out = F.compensated_attention(q, kb, kr, vb, vr, B, H, S, d)
+    n = B * H * S
+    Kb, Kr = O.binary_encode(to_np(kf)), None
+    Kr = O.residual_encode(to_np(kf), Kb)
+    Vb = O.binary_encode(to_np(vf))
+    Vr = O.residual_encode(to_np(vf), Vb)
+    assert_same_bin(bin_from_blob(kb, n, d), Kb, "c1 K")
+    assert_same_res(res_from_blob(kr, n, d), Kr, "c1 K")
+    assert_same_bin(bin_from_blob(vb, n, d), Vb, "c1 V")
+    assert_same_res(res_from_blob(vr, n, d), Vr, "c1 V")
+    _, ref = O.compensated_attention(to_np(q), Kb, Kr, Vb, Vr, B, H, S, return_f32=True)
+    got = to_np(out).astype(np.float32)
+    err, c = close(got, ref, what="c1 vs oracle")
+    exact = F.reference_attention(q, k, v, B, H, S, d).float()
+    _, eref = O.reference_attention(to_np(q), to_np(k), to_np(v), B, H, S, return_f32=True)
+    close(to_np(exact), eref, what="c1 fp16 reference attention vs oracle")
+    g, e = torch.from_numpy(got).view(-1, d), exact.cpu().view(-1, d)
+    cos = torch.nn.functional.cosine_similarity(g, e, dim=1)
+    mae = (g - e).abs().max().item()
+    say(f"c1: vs oracle rel err {err:.2e} cos {c:.7f}; vs fp16 attention mean cos "
+        f"{cos.mean().item():.5f} min {cos.min().item():.5f} max-abs err {mae:.3e}")
     assert cos.mean().item() > 0.9
 
 

@@ -229,6 +229,59 @@ def test_compensated_scores_closed_form():
         np.testing.assert_allclose(o32.reshape(B * H, d)[i], ex, rtol=2e-5, atol=2e-7)
 
 
+def test_binary_attention_closed_form():
+    """Binary attention over random keys in float64 from the decoded signs:
+    score = sq * sk * (sgn q . sgn k) / sqrt(d) with sq = mean|q| and sk the
+    fp16 scale, out = softmax-weighted (+-sv).  Pins the score scale (a
+    dropped scale_q, scale_k or 1/sqrt(d), or a wrong sign convention, moves
+    the weights) and the binary V reconstruction."""
+    rng = np.random.default_rng(17)
+    for d, S in ((64, 200), (128, 300), (256, 150)):
+        B, H = 1, 3
+        Q = (rng.standard_normal((B, H, d)) * 3.0).astype(np.float16)
+        K = (rng.standard_normal((B * H * S, d)) * 1.5 *
+             np.exp(rng.standard_normal((B * H * S, 1)) * 0.5)).astype(np.float16)
+        V = (rng.standard_normal((B * H * S, d)) * 0.5).astype(np.float16)
+        Kb = O.binary_encode(K)
+        Vb = O.binary_encode(V)
+        _, o32 = O.binary_attention(Q, Kb, Vb, B, H, S, return_f32=True)
+        sk = Kb.scale.astype(np.float64).reshape(B * H, S)
+        sv = Vb.scale.astype(np.float64).reshape(B * H, S)
+        sgk = np.where(K.astype(np.float64) >= 0, 1.0, -1.0).reshape(B * H, S, d)
+        sgv = np.where(V.astype(np.float64) >= 0, 1.0, -1.0).reshape(B * H, S, d)
+        for i in range(B * H):
+            q = Q.reshape(-1, d)[i].astype(np.float64)
+            sq = np.abs(q).mean()
+            s = sq * sk[i] * (sgk[i] @ np.where(q >= 0, 1.0, -1.0)) / math.sqrt(d)
+            w = np.exp(s - s.max())
+            ref = (w @ (sv[i][:, None] * sgv[i])) / w.sum()
+            np.testing.assert_allclose(o32.reshape(B * H, d)[i], ref, rtol=2e-5, atol=1e-6)
+        # the scores span many nats, so the test is not blind to their scale
+        assert np.ptp(s) > 4.0
+
+
+def test_torch_cpu_restatement_matches_oracle():
+    """compensated_attention_torch_cpu (the CPU baseline's and the full-size
+    c3 test's fast path) against the numpy oracle on the same encodings."""
+    import torch
+    rng = np.random.default_rng(19)
+    d, S = 128, 700
+    Q = (rng.standard_normal((1, 1, d)) * 0.2).astype(np.float16)
+    K = (rng.standard_normal((S, d)) * 0.2).astype(np.float16)
+    V = (rng.standard_normal((S, d)) * 0.2).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    _, ref = O.compensated_attention(Q, Kb, Kr, Vb, Vr, 1, 1, S, return_f32=True)
+    w64 = lambda w: torch.from_numpy(w.astype(np.int64))
+    got = O.compensated_attention_torch_cpu(
+        torch.from_numpy(Q[0, 0]), w64(Kb.words), torch.from_numpy(Kb.scale),
+        torch.from_numpy(Kr.codes.astype(np.int8)), torch.from_numpy(Kr.scale),
+        w64(Vb.words), torch.from_numpy(Vb.scale), torch.from_numpy(Vr.codes.astype(np.int8)),
+        torch.from_numpy(Vr.scale))
+    np.testing.assert_allclose(got.float().numpy(), ref[0, 0].astype(np.float16).astype(np.float32),
+                               rtol=2e-3, atol=2e-4)
+
+
 def test_attention_special_cases():
     rng = np.random.default_rng(9)
     d = 64
@@ -351,3 +404,25 @@ def test_ring_state():
     slots = [r.append() for _ in range(7)]
     assert slots == [0, 1, 2, 0, 1, 2, 0]
     assert r.filled == 3 and r.write_pos == 1
+
+
+def test_kendall_tau_ab_against_brute_force():
+    """The O(n log n) tau-a / tau-b helper against the reference's O(n^2)
+    pair loop (tests/test_correctness.cu:58-71) on tied and untied data."""
+    from bitcache_amd.workloads import kendall_tau_ab
+    rng = np.random.default_rng(23)
+    for x, y in ((rng.standard_normal(300), rng.standard_normal(300)),
+                 (rng.integers(0, 5, 200).astype(float), rng.integers(0, 7, 200).astype(float))):
+        y = y + 0.5 * x
+        c = dsc = 0
+        for i in range(len(x)):
+            for j in range(i + 1, len(x)):
+                p = (x[i] - x[j]) * (y[i] - y[j])
+                c += p > 0
+                dsc += p < 0
+        n0 = len(x) * (len(x) - 1) / 2
+        n1 = sum(t * (t - 1) / 2 for t in np.unique(x, return_counts=True)[1])
+        n2 = sum(t * (t - 1) / 2 for t in np.unique(y, return_counts=True)[1])
+        ta, tb = kendall_tau_ab(x, y)
+        assert abs(ta - (c - dsc) / n0) < 1e-9
+        assert abs(tb - (c - dsc) / math.sqrt((n0 - n1) * (n0 - n2))) < 1e-9
