@@ -19,6 +19,9 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <mutex>
+#include <vector>
+
 #include "attn.h"
 
 using bc::AttnArgs;
@@ -1066,6 +1069,56 @@ extern "C" int bc_attention_gqa(const void* q, const void* k_bin, const void* k_
     return bc::run_attention(k_res ? MODE_COMP : MODE_BINARY, q, k_bin, k_res, v_bin, v_res, out,
                              batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim, workspace,
                              workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------- allocation-free attention
+// bc_attention_gqa_noalloc keeps its split partials in `scratch`, a file-scope
+// device array (one copy per GPU, held until the process ends) of
+// kNoAllocScratchBytes.  Host code never passes the array's name to a kernel
+// (on the host it is a stand-in, not a device address): each device's
+// address comes from hipGetSymbolAddress on that device's first call and is
+// kept per device.  Calls that overlap on one GPU share the array and race.
+// Every split partial is written by its workgroup before the combine reads
+// it, so nothing needs clearing between calls.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mutex;
+static std::vector<void*> g_scratch_ptrs;   // per device ordinal
+
+static int scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return bc::set_error(BC_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((int)g_scratch_ptrs.size() <= dev) g_scratch_ptrs.resize(dev + 1, nullptr);
+    if (g_scratch_ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return bc::set_error(BC_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptrs[dev] = p;
+    }
+    *out = g_scratch_ptrs[dev];
+    return BC_OK;
+}
+
+extern "C" int bc_attention_gqa_noalloc(const void* q, const void* k_bin, const void* k_res,
+                                        const void* v_bin, const void* v_res, void* out, int batch,
+                                        int n_heads, int n_kv_heads, int seq_len, int kv_stride,
+                                        int head_dim, void* stream) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
+    if (v != BC_OK) return v;
+    const size_t need = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    BC_REQUIRE(need <= kNoAllocScratchBytes, BC_ERR_WORKSPACE,
+               "this shape needs %zu bytes of split partials; the allocation-free entry point "
+               "holds at most %zu (use bc_attention_gqa with a caller workspace)",
+               need, kNoAllocScratchBytes);
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc != BC_OK) return rc;
+    return bc_attention_gqa(q, k_bin, k_res, v_bin, v_res, out, batch, n_heads, n_kv_heads, seq_len,
+                            kv_stride, head_dim, ws, kNoAllocScratchBytes, stream);
 }
 
 // One decode step on a ring cache: the new token's K and V vectors go to

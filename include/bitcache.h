@@ -134,6 +134,18 @@ int bc_attention_gqa(const void* q, const void* k_bin, const void* k_res, const 
                      int seq_len, int kv_stride, int head_dim, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* bc_attention_gqa without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The split
+ * partials live in a library-owned device array of 8 MiB per GPU (held until
+ * the process ends); a shape whose partials need more returns
+ * BC_ERR_WORKSPACE.  The call allocates nothing.  Calls that overlap on one
+ * GPU (two streams, or two threads) share that array and race: serialise
+ * them.  Same results as bc_attention_gqa. */
+int bc_attention_gqa_noalloc(const void* q, const void* k_bin, const void* k_res, const void* v_bin,
+                             const void* v_res, void* out, int batch, int n_heads, int n_kv_heads,
+                             int seq_len, int kv_stride, int head_dim, void* stream);
+
 /* The two phases of bc_attention_gqa, for callers that schedule them
  * separately (e.g. merging partials of a sequence split across devices):
  * bc_attention_partial writes one (max, sum, acc[head_dim]) fp32 partial per
