@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
             for (int w = 0; w < NW; w++) pc += __builtin_popcount(~(qp[g].signs[w] ^ ks.w[w]));
             const float mq = (float)(2 * pc - D);
-            // (scale_q * scale_k) * (2pc - d)   (src/xnor_dot.cuh:179)
+            // (scale_q * scale_k) * (2pc - d)   (src/xnor_dot.cuh:30)
             const float xdot = (qp[g].scale_q * sk) * mq;
             if constexpr (MODE == MODE_ADAPTIVE) {
                 // above the threshold, or equal to it up to the cutoff index
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
 }
 
 // ---------------------------------------------------------------- entropy
-// src/adaptive_precision.cu:196-313.  Tree-order scale_q (thread t of 128
+// src/adaptive_precision.cu:13-130.  Tree-order scale_q (thread t of 128
 // holds |q_t| + |q_{t+128}|, tree s = 64..1), scores without 1/sqrt(d),
 // H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread,
 // merged over the block.  One block of kEntropyThreads per (b, h).

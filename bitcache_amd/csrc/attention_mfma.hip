@@ -767,7 +767,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qd.signs[g][w] ^ r.ks.w[w]));
             }
             const float mq = (float)(2 * pc - D);
-            xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:179)
+            xd[g] = (qd.scale_q[g] * sk) * mq;  // (scale_q * scale_k) * (2pc - d)  (src/xnor_dot.cuh:30)
         }
         // adaptive: the tile's compacted residual positions (as in gather):
         // nsel selected keys, the lane's key at position rpos

@@ -3,8 +3,8 @@
 // One wave64 encodes one vector.  Lane l holds elements l + 64k (k < D/64),
 // which makes the sign words two (or one) wave ballots and lets the scale be
 // reduced in exactly the reference's fp32 order: the reference block has 128
-// threads, thread t summing |x_t| + |x_{t+128}| (src/binary_encode.cu:70-80),
-// followed by a shared-memory tree p[t] += p[t+s], s = 64..1 (:83-88).  Lane l
+// threads, thread t summing |x_t| + |x_{t+128}| (src/binary_encode.cu:31-41),
+// followed by a shared-memory tree p[t] += p[t+s], s = 64..1 (:44-50).  Lane l
 // plays threads l and l+64; the s = 64 step is an in-lane add and the s = 32..1
 // steps are an xor butterfly whose lane-0 value follows the tree's association
 // exactly (fp32 addition is commutative).
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
         } else {
 #pragma unroll
             for (int k = 0; k < K; k++) {
-                // x >= 0.0f: +-0 -> 1, NaN -> 0 (src/binary_encode.cu:74)
+                // x >= 0.0f: +-0 -> 1, NaN -> 0 (src/binary_encode.cu:36)
                 bits[k] = __ballot(active[k] && x[k] >= 0.0f);
             }
             // tree-order abs sum (see file comment).  Lane l is thread l (elements
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
                 if (active[k]) m = fmaxf(m, fabsf(r[k]));
             }
             // fmaxf ignores NaN and is order independent: a butterfly gives the
-            // reference's absmax (src/residual.cu:201-223) in every lane.
+            // reference's absmax (src/residual.cu:30-53) in every lane.
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
             const float absmax = m;

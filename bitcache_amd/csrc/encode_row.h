@@ -6,10 +6,10 @@
 // 64/L such groups, lane = group * L + j, and every lane of the wave calls
 // encode_row (the reductions are DPP / swizzle moves within the group).  The
 // scale sum follows the reference tree exactly: element t = 8j + k sits in
-// lane j, so the tree levels s = 64..8 (src/binary_encode.cu:83-88) pair lane
+// lane j, so the tree levels s = 64..8 (src/binary_encode.cu:44-50) pair lane
 // j with lane j + s/8 (row_shl) and the levels s = 4, 2, 1 are in-lane; d = 256
 // first adds |x_{t+128}| from the lane 16 above (the reference's per-thread
-// loop, :70-80), d = 64 skips the s = 64 level (it adds +0.0).
+// loop, :31-41), d = 64 skips the s = 64 level (it adds +0.0).
 #pragma once
 
 #include "common.h"
@@ -31,7 +31,7 @@ struct EncodeDst {
     uint16_t* rscale_plane;
 };
 
-// __float2int_rn followed by the [-7, 7] clamp of src/residual.cu:237-242; NaN -> 0.
+// __float2int_rn followed by the [-7, 7] clamp of src/residual.cu:67-72; NaN -> 0.
 __device__ __forceinline__ int quant7(float v) {
     if (!(v == v)) return 0;
     float c = fminf(fmaxf(v, -7.0f), 7.0f);
@@ -107,7 +107,7 @@ __device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live
             r[k] = x[k] - (((byte >> k) & 1u) ? s : -s);
             m = fmaxf(m, fabsf(r[k]));
         }
-        // fmaxf ignores NaN and is order independent (src/residual.cu:201-223)
+        // fmaxf ignores NaN and is order independent (src/residual.cu:30-53)
         if constexpr (L == 8) {
             m = fmaxf(m, dpp_f<0x141>(m));   // half mirror
             m = fmaxf(m, dpp_f<0x4E>(m));    // quad 2,3,0,1

@@ -63,13 +63,13 @@ int64_t bc_sizeof_residual_vec(void);
 /* Sign bits + fp16 mean-|x| scale of n_vecs fp16 vectors [n_vecs, head_dim].
  * Blob capacity = n_vecs.  Bit-exact with the reference, including the fp32
  * summation order of the scale.
- * Replaces launch_binary_encode (src/binary_encode.cu:100-118). */
+ * Replaces launch_binary_encode (src/binary_encode.cu:62-80). */
 int bc_binary_encode(const void* src, void* binary_blob, int64_t n_vecs, int head_dim,
                      void* stream);
 
 /* INT4 residual of src against an existing binary blob (its bits and its
  * fp16-rounded scale).  Capacity of both blobs = n_vecs.
- * Replaces launch_residual_encode (src/residual.cu:250-268). */
+ * Replaces launch_residual_encode (src/residual.cu:80-98). */
 int bc_residual_encode(const void* src, const void* binary_blob, void* residual_blob,
                        int64_t n_vecs, int head_dim, void* stream);
 
@@ -77,8 +77,8 @@ int bc_residual_encode(const void* src, const void* binary_blob, void* residual_
  * bc_binary_encode followed by bc_residual_encode; scale_mode 1: the residual is
  * taken against the fp32 mean, as bc_online_encode_token does.
  * residual_blob may be NULL (binary only).  Capacity of both blobs = n_vecs.
- * No counterpart in the reference (it needs two launches, src/binary_encode.cu:100,
- * src/residual.cu:250). */
+ * No counterpart in the reference (it needs two launches, src/binary_encode.cu:62,
+ * src/residual.cu:80). */
 int bc_encode_fused(const void* src, void* binary_blob, void* residual_blob, int64_t n_vecs,
                     int head_dim, int scale_mode, void* stream);
 
@@ -190,8 +190,8 @@ int bc_append_attention(const void* q, const void* k_new, const void* v_new, voi
 
 /* Per-key binary scores xnor_dot * 1/sqrt(d) (float32 [batch, n_heads, seq_len])
  * and/or the XNOR popcounts (int32, same shape); either output may be NULL.
- * Bit-exact.  Exposes the score of src/xnor_dot.cuh:163-180 /
- * src/binary_attention.cu:286-290 (computed there but never returned). */
+ * Bit-exact.  Exposes the score of src/xnor_dot.cuh:14-31 /
+ * src/binary_attention.cu:56, :63 (computed there but never returned). */
 int bc_binary_scores(const void* q, const void* k_bin, float* scores, int32_t* popcounts,
                      int batch, int n_heads, int n_kv_heads, int seq_len, int kv_stride,
                      int head_dim, void* stream);

@@ -14,7 +14,7 @@
 #include <stdint.h>
 #include <string.h>
 
-#define NTHREADS 128 /* blockDim.x of the reference encode kernels (src/binary_encode.cu:110) */
+#define NTHREADS 128 /* blockDim.x of the reference encode kernels (src/binary_encode.cu:72) */
 
 /* ---- IEEE binary16 <-> binary32 ---------------------------------------- */
 float orc_half_to_float(uint16_t h) {
@@ -72,7 +72,7 @@ uint16_t orc_float_to_half(float f) {
 }
 
 /* ---- block simulation of the encode reduction -------------------------- */
-/* src/binary_encode.cu:70-88: per-thread strided |x| sum, then tree. */
+/* src/binary_encode.cu:31-53: per-thread strided |x| sum, then tree. */
 static float block_abs_sum(const float* v, int d) {
     float partial[NTHREADS];
     for (int t = 0; t < NTHREADS; t++) {
@@ -85,7 +85,7 @@ static float block_abs_sum(const float* v, int d) {
     return partial[0];
 }
 
-/* src/residual.cu:201-223: per-thread fmaxf from 0.0f, then fmaxf tree. */
+/* src/residual.cu:30-53: per-thread fmaxf from 0.0f, then fmaxf tree. */
 static float block_abs_max(const float* r, int d) {
     float partial[NTHREADS];
     for (int t = 0; t < NTHREADS; t++) {
@@ -106,7 +106,7 @@ static int f2i_rn(float v) {
     return (int)nearbyintf(v);
 }
 
-/* binary_encode_kernel (src/binary_encode.cu:46-98) for n vectors. */
+/* binary_encode_kernel (src/binary_encode.cu:8-60) for n vectors. */
 void orc_binary_encode(const uint16_t* x, int n, int d, uint32_t* words, uint16_t* scale16,
                        float* mean32) {
     float v[256];
@@ -122,7 +122,7 @@ void orc_binary_encode(const uint16_t* x, int n, int d, uint32_t* words, uint16_
     }
 }
 
-/* residual_encode_kernel (src/residual.cu:179-248) given bits and the scale
+/* residual_encode_kernel (src/residual.cu:9-78) given bits and the scale
  * the residual is taken against (fp16-rounded for the two-step path, fp32 mean
  * for online_encode_token, src/online_encode.cu:74,88). */
 void orc_residual_encode(const uint16_t* x, const uint32_t* words, const float* s, int n, int d,
@@ -163,7 +163,7 @@ void orc_query_prep(const uint16_t* q, int nq, int d, uint32_t* qwords, float* s
     }
 }
 
-/* Tree-order scale_q of compute_head_entropy_kernel (src/adaptive_precision.cu:229-242). */
+/* Tree-order scale_q of compute_head_entropy_kernel (src/adaptive_precision.cu:46-59). */
 void orc_query_prep_tree(const uint16_t* q, int nq, int d, uint32_t* qwords, float* scale_q) {
     float v[256];
     for (int k = 0; k < nq; k++) {
@@ -176,7 +176,7 @@ void orc_query_prep_tree(const uint16_t* q, int nq, int d, uint32_t* qwords, flo
     }
 }
 
-/* xnor_dot (src/xnor_dot.cuh:163-180) for S keys of one query; also popcounts. */
+/* xnor_dot (src/xnor_dot.cuh:14-31) for S keys of one query; also popcounts. */
 void orc_xnor_scores(const uint32_t* qw, float scale_q, const uint32_t* kw, const uint16_t* ks,
                      int S, int d, int32_t* pc_out, float* xdot_out) {
     int nw = d / 32;
@@ -190,7 +190,7 @@ void orc_xnor_scores(const uint32_t* qw, float scale_q, const uint32_t* kw, cons
 }
 
 /* compute_head_entropy_kernel's final combination for one head, two passes
- * over already computed (no 1/sqrt(d)) scores (src/adaptive_precision.cu:251-311). */
+ * over already computed (no 1/sqrt(d)) scores (src/adaptive_precision.cu:65-129). */
 float orc_entropy(const float* score, int S) {
     float M = -1e30f;
     for (int s = 0; s < S; s++) M = fmaxf(M, score[s]);

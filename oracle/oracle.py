@@ -120,10 +120,10 @@ def unpack_nibbles(nib: np.ndarray) -> np.ndarray:
 def _tree_abs_sum(x32: np.ndarray) -> np.ndarray:
     """Sum of |x| in the reference's 128-thread order.
 
-    src/binary_encode.cu:70-88: thread t (blockDim 128) accumulates
+    src/binary_encode.cu:31-53: thread t (blockDim 128) accumulates
     0.0f + |x_t| + |x_{t+128}| + ... sequentially, then a shared-memory tree
     p[t] += p[t+s] for s = 64, 32, ..., 1.  The same order is used by
-    src/online_encode.cu:56-72 and src/adaptive_precision.cu:229-242.
+    src/online_encode.cu:56-72 and src/adaptive_precision.cu:46-59.
     """
     n, d = x32.shape
     p = np.zeros((n, 128), dtype=F32)
@@ -141,10 +141,10 @@ def _tree_abs_sum(x32: np.ndarray) -> np.ndarray:
 
 
 def binary_encode(x: np.ndarray) -> BinaryEnc:
-    """src/binary_encode.cu:46-98.
+    """src/binary_encode.cu:8-60.
 
-    bits: x >= 0.0f (so +-0 -> 1, NaN -> 0)  (:74)
-    scale: fp16(tree_sum|x| / (float)d)       (:91-92), round-to-nearest-even.
+    bits: x >= 0.0f (so +-0 -> 1, NaN -> 0)  (:36)
+    scale: fp16(tree_sum|x| / (float)d)       (:53-54), round-to-nearest-even.
     """
     x = _check_x(x)
     d = x.shape[1]
@@ -159,13 +159,13 @@ def binary_encode(x: np.ndarray) -> BinaryEnc:
 
 
 def _quantize_residual(x32: np.ndarray, bits: np.ndarray, s: np.ndarray) -> ResidualEnc:
-    """Shared body of src/residual.cu:198-247 and src/online_encode.cu:85-119.
+    """Shared body of src/residual.cu:28-77 and src/online_encode.cu:84-119.
 
-    r_i = x_i - (bit_i ? s : -s)          (residual.cu:204-207)
-    absmax = fmaxf over |r_i| from 0.0f   (residual.cu:201,209,215-223) -- NaN ignored
-    inv = absmax > 0 ? 7.0f/absmax : 0    (residual.cu:224)
-    q = clamp(rint_half_even(r * inv), -7, 7), NaN -> 0   (residual.cu:237-242)
-    scale = fp16(absmax)                  (residual.cu:227)
+    r_i = x_i - (bit_i ? s : -s)          (src/residual.cu:34-37)
+    absmax = fmaxf over |r_i| from 0.0f   (src/residual.cu:31,39,44-53) -- NaN ignored
+    inv = absmax > 0 ? 7.0f/absmax : 0    (src/residual.cu:54)
+    q = clamp(rint_half_even(r * inv), -7, 7), NaN -> 0   (src/residual.cu:67-72)
+    scale = fp16(absmax)                  (src/residual.cu:57)
     """
     s = s.astype(F32)[:, None]
     recon = np.where(bits, s, -s).astype(F32)
@@ -184,8 +184,8 @@ def _quantize_residual(x32: np.ndarray, bits: np.ndarray, s: np.ndarray) -> Resi
 
 
 def residual_encode(x: np.ndarray, binary: BinaryEnc) -> ResidualEnc:
-    """Two-step residual: src/residual.cu:179-248.  Uses the *fp16-rounded*
-    binary scale read back from the BinaryVec (:198) and the stored bits (:204)."""
+    """Two-step residual: src/residual.cu:9-78.  Uses the *fp16-rounded*
+    binary scale read back from the BinaryVec (:28) and the stored bits (:34)."""
     x = _check_x(x)
     d = x.shape[1]
     bits = unpack_bits(binary.words, d)
@@ -215,7 +215,7 @@ def encode_fused(x: np.ndarray, fp32_scale: bool = False):
 
 
 def dequant_binary(b: BinaryEnc, d: int) -> np.ndarray:
-    """sign(x) * scale as float32 [n, d] (src/binary_attention.cu:300-304)."""
+    """sign(x) * scale as float32 [n, d] (src/binary_attention.cu:67-73)."""
     bits = unpack_bits(b.words, d)
     s = b.scale.astype(F32)[:, None]
     return np.where(bits, s, -s).astype(F32)
@@ -230,9 +230,9 @@ def dequant_residual(r: ResidualEnc) -> np.ndarray:
 # query preparation
 # ----------------------------------------------------------------------------
 def query_prep(q: np.ndarray):
-    """src/compensated_attention.cu:56-69 / src/binary_attention.cu:257-271.
+    """src/compensated_attention.cu:56-69 / src/binary_attention.cu:24-39.
 
-    q32 = float(Q); sign words via pack_sign_bits (xnor_dot.cuh:36-52, >= 0.0f);
+    q32 = float(Q); sign words via pack_sign_bits (src/xnor_dot.cuh:36-52, >= 0.0f);
     scale_q = (sequential fp32 sum_i |q_i|) / d  -- not rounded to fp16.
     """
     q = np.asarray(q)
@@ -248,7 +248,7 @@ def query_prep(q: np.ndarray):
 
 
 def query_prep_tree(q: np.ndarray):
-    """src/adaptive_precision.cu:224-245: tree-order scale_q (same order as encode)."""
+    """src/adaptive_precision.cu:31-62: tree-order scale_q (same order as encode)."""
     q = np.asarray(q)
     d = q.shape[-1]
     q32 = q.reshape(-1, d).astype(F32)
@@ -267,14 +267,14 @@ def inv_sqrt(d: int) -> np.float32:
 # scores
 # ----------------------------------------------------------------------------
 def popcounts(qwords: np.ndarray, kwords: np.ndarray) -> np.ndarray:
-    """sum_w popc(~(q_w ^ k_w))  (src/xnor_dot.cuh:169-176).
+    """sum_w popc(~(q_w ^ k_w))  (src/xnor_dot.cuh:20-27).
     qwords [W], kwords [S, W] -> int32 [S]."""
     x = ~(kwords.astype(np.uint32) ^ qwords.astype(np.uint32)[None, :])
     return np.bitwise_count(x).astype(np.int32).sum(axis=-1).astype(np.int32)
 
 
 def xnor_dot(scale_q: np.float32, pc: np.ndarray, kscale16: np.ndarray, d: int) -> np.ndarray:
-    """(scale_q * scale_k) * (float)(2*pc - d)  (src/xnor_dot.cuh:177-179)."""
+    """(scale_q * scale_k) * (float)(2*pc - d)  (src/xnor_dot.cuh:28-30)."""
     sk = kscale16.astype(F32)
     return ((F32(scale_q) * sk).astype(F32) * (2 * pc - d).astype(F32)).astype(F32)
 
@@ -294,7 +294,7 @@ def residual_dot(q32: np.ndarray, r: ResidualEnc) -> np.ndarray:
 def binary_scores(Q: np.ndarray, K: BinaryEnc, batch: int, n_heads: int, seq_len: int,
                   n_kv_heads: Optional[int] = None) -> np.ndarray:
     """Per-key binary attention score xnor_dot * inv_sqrt_d, float32 [B, Hq, S]
-    (src/binary_attention.cu:286-290).  K holds B*Hkv*S vectors, head-major."""
+    (src/binary_attention.cu:56, :63).  K holds B*Hkv*S vectors, head-major."""
     hkv = n_heads if n_kv_heads is None else n_kv_heads
     d = Q.shape[-1]
     qw, sq, _ = query_prep(Q.reshape(batch * n_heads, d))
@@ -387,7 +387,7 @@ def compensated_attention(Q, Kb: BinaryEnc, Kr: ResidualEnc, Vb: BinaryEnc, Vr: 
 
 def binary_attention(Q, Kb: BinaryEnc, Vb: BinaryEnc, batch, n_heads, seq_len,
                      n_kv_heads=None, return_f32=False):
-    """src/binary_attention.cu:240-314: scores from xnor_dot only, V = sign*scale."""
+    """src/binary_attention.cu:8-82: scores from xnor_dot only, V = sign*scale."""
     hkv, g = _heads(batch, n_heads, n_kv_heads)
     d = Q.shape[-1]
     sc_all = binary_scores(Q, Kb, batch, n_heads, seq_len, n_kv_heads)
@@ -433,11 +433,11 @@ def compensated_attention_exact_order(Q, Kb, Kr, Vb, Vr, seq_len):
 
 
 def head_entropy(Q, Kb: BinaryEnc, batch, n_heads, seq_len, n_kv_heads=None) -> np.ndarray:
-    """src/adaptive_precision.cu:196-313.
+    """src/adaptive_precision.cu:13-130.
 
-    score = (scale_q * scale_k) * (2pc - d)  -- NO 1/sqrt(d) (:257-258)
-    scale_q in tree order (:229-242)
-    H = (logf(Z) + M) - W / fmaxf(Z, 1e-12)   (:309-310)
+    score = (scale_q * scale_k) * (2pc - d)  -- NO 1/sqrt(d) (:74-75)
+    scale_q in tree order (:46-59)
+    H = (logf(Z) + M) - W / fmaxf(Z, 1e-12)   (:126-127)
     """
     hkv, g = _heads(batch, n_heads, n_kv_heads)
     d = Q.shape[-1]
@@ -491,7 +491,7 @@ def default_top_k(seq_len: int, frac: float = 0.10) -> int:
 
 def topk_key(kscale16: np.ndarray, pc: np.ndarray, d: int) -> np.ndarray:
     """Ranking key: float(scale_k) * (2pc - d), exact in fp32 (<= 19 significant
-    bits), order-equivalent to the reference score (src/xnor_dot.cuh:179) since
+    bits), order-equivalent to the reference score (src/xnor_dot.cuh:30) since
     scale_q > 0.  -0 is canonicalised to +0; NaN ranks below every other key."""
     key = (kscale16.astype(F32) * (2 * pc - d).astype(F32)).astype(F32)
     key = (key + F32(0.0)).astype(F32)
