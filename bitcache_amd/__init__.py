@@ -102,18 +102,26 @@ class BitCache:
         self._write_pos = (self._write_pos + 1) % self.max_seq
         self._filled = min(self._filled + 1, self.max_seq)
 
-    def prefill(self, K: Tensor, V: Tensor) -> None:
-        """Append S tokens at once: K/V [batch, n_kv_heads, S, head_dim] fp16.
+    def prefill(self, K: Tensor, V: Tensor, layout: str = "bhsd") -> None:
+        """Append S tokens at once: K/V [batch, n_kv_heads, S, head_dim] fp16
+        (layout "bhsd") or [batch, S, n_kv_heads, head_dim] (layout "bshd").
 
         Produces the same bytes as S calls to append() (online-encode math,
         src/online_encode.cu:74,88).  The tokens must fit without wrapping."""
-        B, H, S, d = self.batch, self.n_kv_heads, K.shape[2], self.head_dim
-        assert K.shape == (B, H, S, d) and V.shape == (B, H, S, d), "K/V must be [B, Hkv, S, d]"
+        B, H, d = self.batch, self.n_kv_heads, self.head_dim
+        assert layout in ("bhsd", "bshd"), "layout must be 'bhsd' or 'bshd'"
+        S = K.shape[2] if layout == "bhsd" else K.shape[1]
+        shape = (B, H, S, d) if layout == "bhsd" else (B, S, H, d)
+        assert K.shape == shape and V.shape == shape, f"K/V must be {layout} {shape}"
         assert K.dtype == torch.float16 and V.dtype == torch.float16
         assert K.is_contiguous() and V.is_contiguous()
         assert self._write_pos + S <= self.max_seq, "prefill would wrap the ring buffer"
         for src, bin_, res in ((K, self._k_bin, self._k_res), (V, self._v_bin, self._v_res)):
-            _C.encode_into_cache(src, bin_, res, B * H, S, d, self._write_pos, self.max_seq, True)
+            if layout == "bhsd":
+                _C.encode_into_cache(src, bin_, res, B * H, S, d, self._write_pos, self.max_seq, True)
+            else:
+                _C.encode_into_cache_bshd(src, bin_, res, B, S, H, d, self._write_pos,
+                                          self.max_seq, True)
         self._write_pos = (self._write_pos + S) % self.max_seq
         self._filled = min(self._filled + S, self.max_seq)
 

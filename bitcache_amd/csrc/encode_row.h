@@ -38,17 +38,22 @@ __device__ __forceinline__ int quant7(float v) {
     return (int)__builtin_rintf(c);
 }
 
-// Encode the d-element fp16 vector at vec into vector slot dv of dst; lanes
-// with live = false compute along (their group's reductions) but store nothing.
+// This lane's 16-byte slice (elements 8j..8j+7) of the fp16 vector at vec:
+// nontemporal, the wave's vectors are one contiguous run read once.
+__device__ __forceinline__ bc_v4u load_row_slice(const uint16_t* vec, int j) {
+    return __builtin_nontemporal_load((const bc_v4u*)vec + j);
+}
+
+// Encode the d-element fp16 vector whose slice this lane holds (raw, from
+// load_row_slice) into vector slot dv of dst; lanes with live = false compute
+// along (their group's reductions) but store nothing.
 template <int D, int MODE>
-__device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live, const EncodeDst& dst,
-                                           int64_t dv) {
+__device__ __forceinline__ void encode_row_slice(const bc_v4u raw, int j, bool live, const EncodeDst& dst,
+                                                 int64_t dv) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
     constexpr int L = D / 8;        // lanes per vector
     // swizzle pattern that broadcasts lane 0 of each L-lane group (and-mask mode)
     constexpr int BCAST = L == 8 ? 0x18 : (L == 16 ? 0x10 : 0x00);
-    // nontemporal: the wave's vectors are one contiguous run read once
-    const bc_v4u raw = __builtin_nontemporal_load((const bc_v4u*)vec + j);
     const uint32_t hw[4] = {raw[0], raw[1], raw[2], raw[3]};
     float x[8];
 #pragma unroll
@@ -63,19 +68,24 @@ __device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live
     } else {
 #pragma unroll
         for (int k = 0; k < 8; k++) byte |= (x[k] >= 0.0f ? 1u : 0u) << k;  // +-0 -> 1, NaN -> 0
+        // (the first level takes |x| of both operands as source modifiers)
         float p[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]);
         if constexpr (D == 256) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) p[k] = p[k] + swz_f<0x401F>(p[k]);  // + |x_{t+128}|
-        }
-        if constexpr (D >= 128) {
+            for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]) + fabsf(swz_f<0x401F>(x[k]));  // + |x_{t+128}|
 #pragma unroll
             for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x108>(p[k]);   // s = 64
-        }
 #pragma unroll
-        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);       // s = 32
+            for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);   // s = 32
+        } else if constexpr (D == 128) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]) + fabsf(dpp_f<0x108>(x[k]));   // s = 64
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);   // s = 32
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = fabsf(x[k]) + fabsf(dpp_f<0x104>(x[k]));   // s = 32
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x102>(p[k]);       // s = 16
 #pragma unroll
@@ -107,30 +117,40 @@ __device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live
             r[k] = x[k] - (((byte >> k) & 1u) ? s : -s);
             m = fmaxf(m, fabsf(r[k]));
         }
-        // fmaxf ignores NaN and is order independent (src/residual.cu:30-53)
+        // fmaxf ignores NaN and is order independent (src/residual.cu:30-53).
+        // m is a non-negative float, never NaN (the chain starts at 0 and
+        // fmaxf drops NaN operands), and for those the integer order of the
+        // bits is the float order: the lanes merge with integer max
+        uint32_t mb = __builtin_bit_cast(uint32_t, m);
         if constexpr (L == 8) {
-            m = fmaxf(m, dpp_f<0x141>(m));   // half mirror
-            m = fmaxf(m, dpp_f<0x4E>(m));    // quad 2,3,0,1
-            m = fmaxf(m, dpp_f<0xB1>(m));    // quad 1,0,3,2
+            mb = max(mb, dpp_u<0x141>(mb));   // half mirror
+            mb = max(mb, dpp_u<0x4E>(mb));    // quad 2,3,0,1
+            mb = max(mb, dpp_u<0xB1>(mb));    // quad 1,0,3,2
         } else {
-            m = fmaxf(m, dpp_f<0x128>(m));   // row rotations
-            m = fmaxf(m, dpp_f<0x124>(m));
-            m = fmaxf(m, dpp_f<0x122>(m));
-            m = fmaxf(m, dpp_f<0x121>(m));
-            if constexpr (L == 32) m = fmaxf(m, swz_f<0x401F>(m));
+            mb = max(mb, dpp_u<0x128>(mb));   // row rotations
+            mb = max(mb, dpp_u<0x124>(mb));
+            mb = max(mb, dpp_u<0x122>(mb));
+            mb = max(mb, dpp_u<0x121>(mb));
+            if constexpr (L == 32)
+                mb = max(mb, (uint32_t)__builtin_amdgcn_ds_swizzle((int)mb, 0x401F));
         }
-        const float absmax = m;
+        const float absmax = __builtin_bit_cast(float, mb);
         const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
         float y[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) y[k] = r[k] * inv;
-        // a NaN among the scaled residuals makes their sum NaN (otherwise
-        // each is finite and within 7 in magnitude)
-        float t = y[0];
-#pragma unroll
-        for (int k = 1; k < 8; k++) t += y[k];
+        // Every y is finite (and within 7(1 + 2^-23) in magnitude, since
+        // |r| <= absmax) when every x is finite and inv is finite: the x are
+        // then finite, so are s and r.  The packed fp16 sum of the eight x is
+        // finite only if each x is (an overflow merely sends the lanes to the
+        // exact path).
+        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+        const h2_t hs = (__builtin_bit_cast(h2_t, hw[0]) + __builtin_bit_cast(h2_t, hw[1])) +
+                        (__builtin_bit_cast(h2_t, hw[2]) + __builtin_bit_cast(h2_t, hw[3]));
+        const bool finite = __builtin_isfinite(hs[0]) && __builtin_isfinite(hs[1]) &&
+                            __builtin_isfinite(inv);
         uint32_t word = 0;
-        if (__ballot(!(t == t)) == 0ull) {
+        if (__ballot(!finite) == 0ull) {
             // clamp to [-7, 7], then round half to even by adding 1.5 * 2^23
             // (unit in the last place 1): the low nibble of the sum's bits
             // is the code in two's complement, as quant7 gives it
@@ -148,6 +168,12 @@ __device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live
             if (j == 0) dst.rscale_plane[dv] = f2h(absmax);
         }
     }
+}
+
+template <int D, int MODE>
+__device__ __forceinline__ void encode_row(const uint16_t* vec, int j, bool live, const EncodeDst& dst,
+                                           int64_t dv) {
+    encode_row_slice<D, MODE>(load_row_slice(vec, j), j, live, dst, dv);
 }
 
 }  // namespace bc

@@ -218,6 +218,31 @@ void encode_into_cache(torch::Tensor src, torch::Tensor binary_cache,
                  "encode_into_cache");
 }
 
+// [batch, seq, n_heads, head_dim] source (bc_encode_into_cache_bshd)
+void encode_into_cache_bshd(torch::Tensor src, torch::Tensor binary_cache,
+                            std::optional<torch::Tensor> residual_cache, int64_t batch, int64_t seq,
+                            int64_t n_heads, int64_t head_dim, int64_t start_pos, int64_t max_seq,
+                            bool fp32_scale) {
+    BC_CHECK_INPUT(src);
+    check_same_device(src, binary_cache, "binary_cache");
+    TORCH_CHECK(src.numel() == batch * seq * n_heads * head_dim,
+                "src must be [batch, seq, n_heads, head_dim]");
+    TORCH_CHECK(max_seq > 0 && start_pos >= 0 && start_pos + seq <= max_seq,
+                "start_pos + seq must fit in max_seq");
+    const int64_t cap = batch * n_heads * max_seq;
+    void* bin = blob_exact(binary_cache, cap, bc_sizeof_binary_vec(), "binary_cache");
+    void* res = nullptr;
+    if (residual_cache.has_value()) {
+        check_same_device(src, *residual_cache, "residual_cache");
+        res = blob_exact(*residual_cache, cap, bc_sizeof_residual_vec(), "residual_cache");
+    }
+    c10::DeviceGuard guard(src.device());
+    check_status(bc_encode_into_cache_bshd(src.data_ptr(), bin, res, (int)batch, (int)seq,
+                                           (int)n_heads, (int)head_dim, (int)start_pos,
+                                           (int)max_seq, fp32_scale ? 1 : 0, stream_of(src)),
+                 "encode_into_cache_bshd");
+}
+
 // ------------------------------------------------------------------ attention
 void check_q(const torch::Tensor& Q, int64_t batch, int64_t n_heads, int64_t d) {
     BC_CHECK_INPUT(Q);
@@ -557,6 +582,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("fp32_scale") = false);
     m.def("online_encode_kv", &online_encode_kv, "K and V token encode in one launch");
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
+    m.def("encode_into_cache_bshd", &encode_into_cache_bshd,
+          "Bulk prefill into ring caches from a [batch, seq, heads, d] source");
     m.def("attention", &attention, "GQA / ring-stride binary or compensated attention");
     m.def("append_attention", &append_attention, "One decode step: ring-cache append + attention");
     m.def("head_mode_attention", &head_mode_attention, "Per-head binary / compensated attention");

@@ -99,6 +99,15 @@ int bc_encode_into_cache(const void* src, void* binary_cache, void* residual_cac
                          int seq, int head_dim, int start_pos, int max_seq, int scale_mode,
                          void* stream);
 
+/* bc_encode_into_cache for a source in the [batch, seq, n_heads, head_dim]
+ * layout many model stacks hold K/V in: vector (b, s, h) lands in slot
+ * start_pos + s of row b*n_heads + h (caches of capacity batch*n_heads*max_seq),
+ * with the same bytes as bc_encode_into_cache of the [batch, n_heads, seq,
+ * head_dim] transpose.  No counterpart in the reference. */
+int bc_encode_into_cache_bshd(const void* src, void* binary_cache, void* residual_cache, int batch,
+                              int seq, int n_heads, int head_dim, int start_pos, int max_seq,
+                              int scale_mode, void* stream);
+
 /* K and V of one decode step in a single launch (same semantics as two
  * bc_online_encode_token calls).  k_res / v_res may be NULL. */
 int bc_online_encode_kv(const void* k, const void* v, void* k_bin, void* k_res, void* v_bin,

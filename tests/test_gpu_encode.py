@@ -140,6 +140,63 @@ def test_encode_into_cache_equals_appends():
     assert torch.equal(kb, kb2) and torch.equal(kr, kr2)
 
 
+@pytest.mark.parametrize("B,S,H,d,max_seq,start,res", [
+    (2, 300, 4, 128, 320, 7, True),
+    (3, 77, 8, 64, 77, 0, True),
+    (1, 513, 2, 256, 600, 40, True),
+    (2, 50, 3, 96, 64, 5, True),      # head dim of the one-vector-per-wave encoder
+    (2, 33, 5, 128, 40, 1, False),    # binary-only cache, odd head count
+])
+def test_encode_into_cache_bshd(B, S, H, d, max_seq, start, res):
+    """[batch, seq, heads, d] prefill source: the same cache bytes as the
+    [batch, heads, seq, d] prefill of its transpose (online-encode math and
+    two-step math), and as appending its tokens one by one."""
+    import bitcache_amd as bc
+    say(f"case encode_into_cache_bshd B={B} S={S} H={H} d={d} start={start} res={res}")
+    rows, n = B * H, B * H * max_seq
+    rng = np.random.default_rng(S + d)
+    x = (rng.standard_normal((B, S, H, d)) * 0.2).astype(np.float16)
+    xt = torch.from_numpy(x).cuda()
+    xh = xt.permute(0, 2, 1, 3).contiguous()
+    for fp32 in (True, False):
+        blobs = []
+        for layout in ("bshd", "bhsd"):
+            kb = torch.zeros(n * 36, dtype=torch.uint8, device="cuda")
+            kr = torch.zeros(n * 130, dtype=torch.uint8, device="cuda") if res else None
+            if layout == "bshd":
+                bc._C.encode_into_cache_bshd(xt, kb, kr, B, S, H, d, start, max_seq, fp32)
+            else:
+                bc._C.encode_into_cache(xh, kb, kr, rows, S, d, start, max_seq, fp32)
+            blobs.append((kb, kr))
+        assert torch.equal(blobs[0][0], blobs[1][0])
+        if res:
+            assert torch.equal(blobs[0][1], blobs[1][1])
+    # == token-by-token appends (online-encode math)
+    kb2 = torch.zeros(n * 36, dtype=torch.uint8, device="cuda")
+    kr2 = torch.zeros(n * 130, dtype=torch.uint8, device="cuda") if res else None
+    for s in range(S):
+        bc._C.online_encode_token(xt[:, s].contiguous(), kb2, kr2, B, H, d, start + s, max_seq)
+    kb, kr = torch.zeros_like(kb2), (torch.zeros_like(kr2) if res else None)
+    bc._C.encode_into_cache_bshd(xt, kb, kr, B, S, H, d, start, max_seq, True)
+    assert torch.equal(kb, kb2) and (not res or torch.equal(kr, kr2))
+
+
+def test_bitcache_prefill_bshd():
+    from bitcache_amd import BitCache
+    say("case bitcache prefill bshd")
+    B, Hq, Hkv, S, d = 2, 8, 2, 200, 128
+    rng = np.random.default_rng(4)
+    k = torch.from_numpy((rng.standard_normal((B, S, Hkv, d)) * 0.2).astype(np.float16)).cuda()
+    v = torch.from_numpy((rng.standard_normal((B, S, Hkv, d)) * 0.2).astype(np.float16)).cuda()
+    a = BitCache(B, Hq, d, 256, n_kv_heads=Hkv)
+    b = BitCache(B, Hq, d, 256, n_kv_heads=Hkv)
+    a.prefill(k, v, layout="bshd")
+    b.prefill(k.permute(0, 2, 1, 3).contiguous(), v.permute(0, 2, 1, 3).contiguous())
+    for x, y in ((a._k_bin, b._k_bin), (a._v_bin, b._v_bin), (a._k_res, b._k_res), (a._v_res, b._v_res)):
+        assert torch.equal(x, y)
+    assert a.seq_len == b.seq_len == S
+
+
 def test_reference_layout_conversion(F):
     from bitcache_amd import layout
     say("case layout_conversion")
