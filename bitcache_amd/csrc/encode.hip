@@ -10,6 +10,8 @@
 // exactly (fp32 addition is commutative).
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "encode_row.h"
 
@@ -18,8 +20,8 @@ using bc::ENC_BINARY;
 using bc::ENC_FUSED_FP16;
 using bc::ENC_FUSED_FP32;
 using bc::ENC_RESIDUAL_ONLY;
+using bc::ENC_TRAFFIC;
 using bc::EncodeDst;
-using bc::encode_row;
 using bc::quant7;
 
 // Unsigned 32-bit division by an invariant divisor 1 <= d <= 2^31 (the
@@ -168,15 +170,215 @@ __global__ __launch_bounds__(256) void encode_kernel(EncodeJob j0, EncodeJob j1)
 }
 
 // ---------------------------------------------------------------------------
-// Row-parallel encoder for d in {64, 128, 256}: L = d/8 lanes per vector, each
-// lane holding 8 consecutive elements (one 16-byte load), so a wave encodes
-// 64/L vectors at once with coalesced loads and stores and all reductions on
-// DPP / swizzle lane moves (encode_row in encode_row.h).  Same arithmetic as
-// encode_kernel.
+// Two-slice row encoder for d in {64, 128, 256}: P = d/16 lanes per vector,
+// lane j (0 <= j < P) of its group holding slice A = elements 8j..8j+7 and
+// slice B = elements d/2 + 8j..d/2 + 8j + 7 (two 16-byte loads).  The
+// reference's first reduction level pairs t with t + d/2 (for d = 256 the
+// per-thread |x_t| + |x_{t+128}| of src/binary_encode.cu:31-41, for d = 128
+// the s = 64 step of :44-50, for d = 64 the s = 32 step after an s = 64 step
+// that adds +0.0), so it is one in-lane add per element pair with no lane
+// idle; the levels s = d/4 .. 8 pair lane j with lane j + s/8 (DPP row_shl)
+// and s = 4, 2, 1 are in-lane, the reference tree's association exactly.
+// Half as many lanes per vector as a one-slice layout halves the per-vector
+// work (lane reductions, the division, the stores) per element.
+//
+// Quantisation fast path: when every x of the wave's vectors is finite (the
+// abs sum is finite exactly then: |x| <= 65504 and d <= 256) and 7 / absmax
+// is finite, |y| = |r * inv| <= 7 (1 + 2^-24)^2 < 7.5 because |r| <= absmax,
+// so the clamp to [-7, 7] of src/residual.cu:67-72 never applies and
+// __float2int_rn(y) is y + 12582920.0f rounded to an integer (ulp 1 there;
+// 12582920 = 1.5 * 2^23 + 8 is even, so ties go to even as in rint): the
+// low byte of its bits is rint(y) + 8 in [1, 15] with a clear high nibble,
+// and nibble pairs are (c1 << 4) | c0 in the low byte, gathered with byte
+// permutes; xor 0x8 per nibble turns the offset code into two's complement.
+// Any other wave takes quant7 per element.
+//
+// |a| + |b| and x - (+-s) take the fp16 elements straight into v_fma_mix
+// (fma(a, 1, b) is the single-rounded sum, equal to the fp32 add of the
+// exactly converted halves); `one` is an fp16 1.0 the compiler cannot fold,
+// so it keeps the fma rather than rewriting it to convert + add.
+template <int D, int MODE>
+__device__ __forceinline__ void encode_two_slices(const bc_v4u ra, const bc_v4u rb, int j, bool live,
+                                                  const EncodeDst& dst, int64_t dv, _Float16 one) {
+    static_assert(D == 64 || D == 128 || D == 256, "two-slice encoder: d in {64, 128, 256}");
+    constexpr int P = D / 16;
+    if constexpr (MODE == ENC_TRAFFIC) {
+        // the fused encoder's loads and stores with no arithmetic
+        const uint32_t x = ra[0] ^ rb[1], y = ra[1] ^ rb[0];
+        if (live) {
+            uint8_t* srow = dst.sign_plane + dv * (D / 8);
+            if ((j & 3) == 0) {
+                ((uint32_t*)srow)[j >> 2] = x;
+                ((uint32_t*)(srow + P))[j >> 2] = y;
+            }
+            uint32_t* crow = (uint32_t*)(dst.code_plane + dv * (D / 2));
+            crow[j] = ra[2] ^ rb[3];
+            crow[P + j] = ra[3] ^ rb[2];
+            if (j == 0) {
+                dst.scale_plane[dv] = (uint16_t)x;
+                dst.rscale_plane[dv] = (uint16_t)y;
+            }
+        }
+        return;
+    }
+    // swizzle (and-mask mode) that broadcasts lane 0 of each P-lane group
+    constexpr int BCAST = P == 4 ? 0x1C : (P == 8 ? 0x18 : 0x10);
+    _Float16 xa[8], xb[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        xa[k] = __builtin_bit_cast(_Float16, (uint16_t)(ra[k >> 1] >> (16 * (k & 1))));
+        xb[k] = __builtin_bit_cast(_Float16, (uint16_t)(rb[k >> 1] >> (16 * (k & 1))));
+    }
+    const float onef = (float)one;
+    bool pa[8], pb[8];      // x >= 0: +-0 -> 1, NaN -> 0 (src/binary_encode.cu:36)
+    uint32_t byte_a = 0, byte_b = 0;
+    float s;
+    float total_abs = 0.0f;
+    if constexpr (MODE == ENC_RESIDUAL_ONLY) {
+        const uint8_t* sp = dst.sign_plane + dv * (D / 8);
+        byte_a = sp[j];
+        byte_b = sp[P + j];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            pa[k] = (byte_a >> k) & 1u;
+            pb[k] = (byte_b >> k) & 1u;
+        }
+        s = h2f(dst.scale_plane[dv]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            pa[k] = xa[k] >= (_Float16)0.0f;
+            pb[k] = xb[k] >= (_Float16)0.0f;
+            byte_a |= (pa[k] ? 1u : 0u) << k;
+            byte_b |= (pb[k] ? 1u : 0u) << k;
+        }
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            p[k] = __builtin_fmaf((float)__builtin_fabsf16(xa[k]), onef, (float)__builtin_fabsf16(xb[k]));
+        if constexpr (P == 16) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x108>(p[k]);   // s = 64
+        }
+        if constexpr (P >= 8) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x104>(p[k]);   // s = 32
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x102>(p[k]);       // s = 16
+#pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = p[k] + dpp_f<0x101>(p[k]);       // s = 8
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = p[k] + p[k + 4];                  // s = 4
+        p[0] = p[0] + p[2];
+        p[1] = p[1] + p[3];                                                   // s = 2
+        p[0] = p[0] + p[1];                                                   // s = 1
+        total_abs = swz_f<BCAST>(p[0]);
+        const float mean = total_abs / (float)D;
+        if constexpr (MODE == ENC_FUSED_FP16) s = h2f(f2h(mean));
+        else s = mean;
+        // sign bytes: A of lanes j..j+3 -> row dword j/4, B -> dword P/4 + j/4
+        const uint32_t v = byte_a | (byte_b << 16);
+        const uint32_t u = v | (dpp_u<0x101>(v) << 8);      // A, B bytes of lanes j, j+1
+        const uint32_t w = dpp_u<0x102>(u);                  // the same for lanes j+2, j+3
+        if (live) {
+            uint8_t* srow = dst.sign_plane + dv * (D / 8);
+            if ((j & 3) == 0) {
+                ((uint32_t*)srow)[j >> 2] = __builtin_amdgcn_perm(w, u, 0x05040100u);
+                ((uint32_t*)(srow + P))[j >> 2] = __builtin_amdgcn_perm(w, u, 0x07060302u);
+            }
+            if (j == 0) dst.scale_plane[dv] = f2h(mean);
+        }
+    }
+
+    if constexpr (MODE != ENC_BINARY) {
+        if (dst.code_plane == nullptr) return;
+        float r_a[8], r_b[8];
+        float m = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            r_a[k] = __builtin_fmaf((float)xa[k], onef, pa[k] ? -s : s);
+            r_b[k] = __builtin_fmaf((float)xb[k], onef, pb[k] ? -s : s);
+            m = fmaxf(m, fabsf(r_a[k]));
+            m = fmaxf(m, fabsf(r_b[k]));
+        }
+        // fmaxf ignores NaN and is order independent (src/residual.cu:30-53);
+        // m is a non-negative float, never NaN, and for those the integer
+        // order of the bits is the float order: lanes merge with integer max
+        uint32_t mb = __builtin_bit_cast(uint32_t, m);
+        if constexpr (P == 4) {
+            mb = max(mb, dpp_u<0xB1>(mb));    // quad 1,0,3,2
+            mb = max(mb, dpp_u<0x4E>(mb));    // quad 2,3,0,1
+        } else if constexpr (P == 8) {
+            mb = max(mb, dpp_u<0x141>(mb));   // half mirror
+            mb = max(mb, dpp_u<0x4E>(mb));
+            mb = max(mb, dpp_u<0xB1>(mb));
+        } else {
+            mb = max(mb, dpp_u<0x128>(mb));   // row rotations
+            mb = max(mb, dpp_u<0x124>(mb));
+            mb = max(mb, dpp_u<0x122>(mb));
+            mb = max(mb, dpp_u<0x121>(mb));
+        }
+        const float absmax = __builtin_bit_cast(float, mb);
+        const float inv = absmax > 0.0f ? 7.0f / absmax : 0.0f;
+        float y_a[8], y_b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            y_a[k] = r_a[k] * inv;
+            y_b[k] = r_b[k] * inv;
+        }
+        bool finite;
+        if constexpr (MODE == ENC_RESIDUAL_ONLY) {
+            // the packed fp16 sum of the elements is finite only if each is
+            typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+            h2_t hs = __builtin_bit_cast(h2_t, ra[0]);
+#pragma unroll
+            for (int i = 1; i < 4; i++) hs = hs + __builtin_bit_cast(h2_t, ra[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) hs = hs + __builtin_bit_cast(h2_t, rb[i]);
+            finite = __builtin_isfinite(hs[0]) && __builtin_isfinite(hs[1]) && __builtin_isfinite(s) &&
+                     __builtin_isfinite(inv);
+        } else {
+            finite = __builtin_isfinite(total_abs) && __builtin_isfinite(inv);
+        }
+        uint32_t word_a, word_b;
+        if (__ballot(!finite) == 0ull) {
+            auto pack = [](const float* y) -> uint32_t {
+                uint32_t c[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) c[k] = __builtin_bit_cast(uint32_t, y[k] + 12582920.0f);
+                const uint32_t p0 = (c[1] << 4) | c[0], p1 = (c[3] << 4) | c[2];
+                const uint32_t p2 = (c[5] << 4) | c[4], p3 = (c[7] << 4) | c[6];
+                const uint32_t t0 = __builtin_amdgcn_perm(p1, p0, 0x0C0C0400u);   // p0.b0, p1.b0
+                const uint32_t t1 = __builtin_amdgcn_perm(p3, p2, 0x0C0C0400u);   // p2.b0, p3.b0
+                return __builtin_amdgcn_perm(t1, t0, 0x05040100u) ^ 0x88888888u;
+            };
+            word_a = pack(y_a);
+            word_b = pack(y_b);
+        } else {
+            word_a = word_b = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                word_a |= ((uint32_t)quant7(y_a[k]) & 0xFu) << (4 * k);
+                word_b |= ((uint32_t)quant7(y_b[k]) & 0xFu) << (4 * k);
+            }
+        }
+        if (live) {
+            uint32_t* crow = (uint32_t*)(dst.code_plane + dv * (D / 2));
+            crow[j] = word_a;
+            crow[P + j] = word_b;
+            if (j == 0) dst.rscale_plane[dv] = f2h(absmax);
+        }
+    }
+}
+
+// Row-parallel encoder for d in {64, 128, 256}: 64/P vectors per wave
+// iteration (encode_two_slices), coalesced loads and stores, all reductions
+// on DPP / swizzle lane moves.  Same results as encode_kernel.
 template <int D, int MODE>
 __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
-    constexpr int L = D / 8;        // lanes per vector
+    constexpr int L = D / 16;       // lanes per vector
     constexpr int VPW = 64 / L;     // vectors per wave
     const int lane = threadIdx.x & 63;
     const int sub = lane / L, j = lane % L;
@@ -218,25 +420,36 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
         auto base_of = [&](int64_t t) {
             return ((t / kRun) * nwaves + wave_id) * (kRun * VPW) + (t % kRun) * VPW;
         };
+        // fp16 1.0 hidden from constant folding (see encode_two_slices)
+        _Float16 one = (_Float16)1.0f;
+        asm volatile("" : "+v"(one));
+        // slices A and B of this lane's vector (nontemporal: each wave's
+        // vectors are one contiguous run read once)
+        auto load = [&](int64_t b, bc_v4u& a, bc_v4u& bb) {
+            const bc_v4u* p = (const bc_v4u*)(J.src + vec_of(b) * D) + j;
+            a = __builtin_nontemporal_load(p);
+            bb = __builtin_nontemporal_load(p + D / 16);
+        };
         // two register sets used in turn (a copy between them would wait for
         // the load in flight); the prefetch is issued unconditionally (past
-        // the last iteration it reloads the current slice) so that the wait
+        // the last iteration it reloads the current slices) so that the wait
         // before each encode leaves it in flight
         int64_t t = 0;
         int64_t base = base_of(0);
         if (base >= J.n) continue;
-        bc_v4u ra = bc::load_row_slice(J.src + vec_of(base) * D, j), rb;
+        bc_v4u ra, rb, qa, qb;
+        load(base, ra, rb);
         for (;;) {
             int64_t nb = base_of(t + 1);
             bool more = nb < J.n;   // (wave-uniform)
-            rb = bc::load_row_slice(J.src + vec_of(more ? nb : base) * D, j);
-            bc::encode_row_slice<D, MODE>(ra, j, base + sub < J.n, dst, dest_for(base));
+            load(more ? nb : base, qa, qb);
+            encode_two_slices<D, MODE>(ra, rb, j, base + sub < J.n, dst, dest_for(base), one);
             if (!more) break;
             base = nb;
             nb = base_of(t + 2);
             more = nb < J.n;
-            ra = bc::load_row_slice(J.src + vec_of(more ? nb : base) * D, j);
-            bc::encode_row_slice<D, MODE>(rb, j, base + sub < J.n, dst, dest_for(base));
+            load(more ? nb : base, ra, rb);
+            encode_two_slices<D, MODE>(qa, qb, j, base + sub < J.n, dst, dest_for(base), one);
             if (!more) break;
             base = nb;
             t += 2;
@@ -250,36 +463,63 @@ int grid_for(int64_t nvec) {
     return (int)(want < cap ? (want < 1 ? 1 : want) : cap);
 }
 
+// Blocks per CU of the row encoder: 3 (12 waves per CU) measured fastest for
+// its mixed read / write stream (2: 1.27 ms, 3: 1.17 ms, 4: 1.19 ms, 16:
+// 1.21 ms for 16.8M vectors of d = 128); more waves in flight add contention
+// in the memory system, fewer leave the loads' latency exposed.
+constexpr int kEncodeBlocksPerCU = 3;
+
+// 256-thread blocks of `kernel` resident per CU (occupancy query, once per
+// kernel; at least 1)
+template <int MODE>
+int resident_blocks(int d, void (*kernel)(EncodeJob, EncodeJob)) {
+    static std::mutex mu;
+    static int cached[3] = {0, 0, 0};
+    const int slot = d == 64 ? 0 : (d == 128 ? 1 : 2);
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached[slot] == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n < 1) n = 1;
+        cached[slot] = n;
+    }
+    return cached[slot];
+}
+
 template <int MODE>
 int launch_encode(int d, const EncodeJob& a, const EncodeJob& b, hipStream_t st) {
     if (d == 64 || d == 128 || d == 256) {
-        // row encoder: 64/L vectors per wave, 4 waves per block, runs of 16
-        // wave iterations, grid-stride
-        const int64_t vpb = 4 * (64 / (d / 8)) * 16;
+        // row encoder: 64/P vectors per wave, 4 waves per block, runs of 16
+        // wave iterations, grid-stride over at most kEncodeBlocksPerCU blocks
+        // per CU, all resident at once (a grid of several rounds ends with a
+        // round at low occupancy)
+        const int64_t vpb = 4 * (64 / (d / 16)) * 16;
         const int64_t want = (a.n + b.n + vpb - 1) / vpb;
-        const int64_t cap = (int64_t)bc::device_cu_count() * 16;
+        auto kernel = d == 64 ? encode_rows_kernel<64, MODE>
+                              : (d == 128 ? encode_rows_kernel<128, MODE> : encode_rows_kernel<256, MODE>);
+        const int per_cu = resident_blocks<MODE>(d, kernel);
+        const int64_t cap =
+            (int64_t)bc::device_cu_count() * (per_cu < kEncodeBlocksPerCU ? per_cu : kEncodeBlocksPerCU);
         const int grid = (int)(want < cap ? (want < 1 ? 1 : want) : cap);
-        if (d == 64)
-            hipLaunchKernelGGL((encode_rows_kernel<64, MODE>), dim3(grid), dim3(256), 0, st, a, b);
-        else if (d == 128)
-            hipLaunchKernelGGL((encode_rows_kernel<128, MODE>), dim3(grid), dim3(256), 0, st, a, b);
-        else
-            hipLaunchKernelGGL((encode_rows_kernel<256, MODE>), dim3(grid), dim3(256), 0, st, a, b);
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, a, b);
         return bc::check_launch("encode");
     }
-    const int grid = grid_for(a.n + b.n);
-    switch (d) {
-#define BC_CASE(DD)                                                                       \
-    case DD:                                                                              \
-        hipLaunchKernelGGL((encode_kernel<DD, MODE>), dim3(grid), dim3(256), 0, st, a, b); \
+    if constexpr (MODE == ENC_TRAFFIC) {
+        return bc::set_error(BC_ERR_UNSUPPORTED, "traffic probe: head_dim %d unsupported", d);
+    } else {
+        const int grid = grid_for(a.n + b.n);
+        switch (d) {
+#define BC_CASE(DD)                                                                           \
+    case DD:                                                                                  \
+        hipLaunchKernelGGL((encode_kernel<DD, MODE>), dim3(grid), dim3(256), 0, st, a, b);     \
         break;
-        BC_CASE(32) BC_CASE(64) BC_CASE(96) BC_CASE(128) BC_CASE(160) BC_CASE(192) BC_CASE(224)
-        BC_CASE(256)
+            BC_CASE(32) BC_CASE(64) BC_CASE(96) BC_CASE(128) BC_CASE(160) BC_CASE(192) BC_CASE(224)
+            BC_CASE(256)
 #undef BC_CASE
-        default:
-            return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d unsupported", d);
+            default:
+                return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d unsupported", d);
+        }
+        return bc::check_launch("encode");
     }
-    return bc::check_launch("encode");
 }
 
 EncodeJob make_job(const void* src, void* bin, void* res, int64_t n, int64_t cap, int d,
@@ -343,6 +583,19 @@ extern "C" int bc_encode_fused(const void* src, void* binary_blob, void* residua
     if (!residual_blob) return launch_encode<ENC_BINARY>(head_dim, a, b, (hipStream_t)stream);
     if (scale_mode == 0) return launch_encode<ENC_FUSED_FP16>(head_dim, a, b, (hipStream_t)stream);
     return launch_encode<ENC_FUSED_FP32>(head_dim, a, b, (hipStream_t)stream);
+}
+
+extern "C" int bc_encode_traffic_probe(const void* src, void* binary_blob, void* residual_blob,
+                                       int64_t n_vecs, int head_dim, void* stream) {
+    BC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, BC_ERR_UNSUPPORTED,
+               "traffic probe: head_dim must be 64, 128 or 256, got %d", head_dim);
+    BC_REQUIRE(n_vecs >= 0, BC_ERR_INVALID_ARGUMENT, "n_vecs < 0");
+    if (n_vecs == 0) return BC_OK;
+    BC_REQUIRE(src && binary_blob && residual_blob, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    BC_REQUIRE(n_vecs <= INT32_MAX, BC_ERR_INVALID_ARGUMENT, "n_vecs above 2^31 - 1");
+    EncodeJob a = make_job(src, binary_blob, residual_blob, n_vecs, n_vecs, head_dim, 1, 1, 1, 0);
+    EncodeJob b{};
+    return launch_encode<ENC_TRAFFIC>(head_dim, a, b, (hipStream_t)stream);
 }
 
 static int online_common(const void* k, const void* v, void* k_bin, void* k_res, void* v_bin,

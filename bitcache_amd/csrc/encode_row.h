@@ -21,6 +21,7 @@ enum EncodeMode : int {
     ENC_FUSED_FP16 = 1,     // bits + scale + residual against the fp16 scale (two-step semantics)
     ENC_FUSED_FP32 = 2,     // bits + scale + residual against the fp32 mean (online semantics)
     ENC_RESIDUAL_ONLY = 3,  // residual against bits + fp16 scale read from a binary blob
+    ENC_TRAFFIC = 4,        // the fused encoder's loads and stores, no arithmetic (memory floor)
 };
 
 // Planes of a destination blob pair (code_plane may be null: binary only).

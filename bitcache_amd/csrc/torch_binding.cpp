@@ -144,6 +144,25 @@ std::tuple<torch::Tensor, torch::Tensor> encode_fused(torch::Tensor src, bool fp
     return {bin, res};
 }
 
+// The memory floor of encode_fused: same kernel, loads and stores, no
+// arithmetic; bin / res are blobs of capacity n_vecs (their bytes become
+// meaningless).
+void encode_traffic_probe(torch::Tensor src, torch::Tensor bin, torch::Tensor res) {
+    BC_CHECK_INPUT(src);
+    TORCH_CHECK(src.dim() == 2, "src must be 2D [n_vecs, head_dim]");
+    const int64_t n = src.size(0);
+    const int64_t d = src.size(1);
+    TORCH_CHECK(bin.is_cuda() && res.is_cuda() && bin.is_contiguous() && res.is_contiguous() &&
+                    bin.dtype() == torch::kUInt8 && res.dtype() == torch::kUInt8,
+                "bin / res must be contiguous uint8 device tensors");
+    TORCH_CHECK(bin.numel() == n * bc_sizeof_binary_vec() && res.numel() == n * bc_sizeof_residual_vec(),
+                "bin / res must be blobs of capacity n_vecs");
+    c10::DeviceGuard guard(src.device());
+    check_status(bc_encode_traffic_probe(src.data_ptr(), bin.data_ptr(), res.data_ptr(), n, (int)d,
+                                         stream_of(src)),
+                 "encode_traffic_probe");
+}
+
 void check_kv_token(const torch::Tensor& kv, int64_t batch, int64_t n_heads, int64_t d) {
     BC_CHECK_INPUT(kv);
     TORCH_CHECK(kv.numel() == batch * n_heads * d, "kv must hold batch*n_heads*head_dim values");
@@ -580,6 +599,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     // extensions
     m.def("encode_fused", &encode_fused, "Binary + residual encode in one pass", py::arg("src"),
           py::arg("fp32_scale") = false);
+    m.def("encode_traffic_probe", &encode_traffic_probe,
+          "encode_fused's loads and stores without its arithmetic (memory floor)");
     m.def("online_encode_kv", &online_encode_kv, "K and V token encode in one launch");
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
     m.def("encode_into_cache_bshd", &encode_into_cache_bshd,

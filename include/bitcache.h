@@ -114,6 +114,14 @@ int bc_online_encode_kv(const void* k, const void* v, void* k_bin, void* k_res, 
                         void* v_res, int batch, int n_heads, int head_dim, int64_t current_len,
                         int max_seq, void* stream);
 
+/* Memory floor of bc_encode_fused: the same kernel, grid, loads and stores
+ * with the arithmetic left out, so its time is what the access pattern alone
+ * costs.  Writes meaningless bytes into both blobs (capacity n_vecs each).
+ * head_dim 64, 128 or 256.  No counterpart in the reference; a measurement
+ * aid for benchmarks. */
+int bc_encode_traffic_probe(const void* src, void* binary_blob, void* residual_blob,
+                            int64_t n_vecs, int head_dim, void* stream);
+
 /* ---- attention -------------------------------------------------------------- */
 /* Bytes of scratch the attention entry points need for this shape on the
  * current device (split-KV partial results).  Callers allocate it; it may be

@@ -87,6 +87,12 @@ def test_encode_argument_errors(lib, no_gpu):
     e.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                   ctypes.c_int, P]
     assert e(fake, fake, fake, 2, 10, 128, 8, 16, 1, None) == BC_ERR_INVALID_ARGUMENT  # overflows ring
+    t = lib.bc_encode_traffic_probe
+    t.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, P]
+    assert t(fake, fake, fake, 10, 96, None) == BC_ERR_UNSUPPORTED        # row encoder dims only
+    assert t(fake, fake, fake, -1, 128, None) == BC_ERR_INVALID_ARGUMENT
+    assert t(fake, None, fake, 10, 128, None) == BC_ERR_INVALID_ARGUMENT
+    assert t(None, None, None, 0, 128, None) == BC_OK
 
 
 def test_attention_argument_errors(lib, no_gpu):

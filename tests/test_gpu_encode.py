@@ -29,6 +29,16 @@ def rand_x(n, d, seed):
         x[0] = 0.5
         x[1, ::2] = np.float16(-0.0)
         x[2, :3] = [np.inf, -np.inf, np.nan]
+    if n >= 200:
+        # fp16 subnormals only (7 / absmax may overflow), the largest finite
+        # magnitudes, zeros of both signs, and small integers (exact ties of
+        # r * 7 / absmax at .5), each far from the NaN row so that whole waves
+        # of such vectors take the fast quantisation path
+        x[64] = (rng.integers(-1023, 1024, d) * 2.0 ** -24).astype(np.float16)
+        x[65] = rng.choice([-65504.0, 65504.0, -32768.0, 1.0], d).astype(np.float16)
+        x[66] = np.where(rng.random(d) < 0.5, np.float16(-0.0), np.float16(0.0))
+        x[67] = np.float16(2.0 ** -24)
+        x[100:200] = rng.integers(-8, 9, (100, d)).astype(np.float16)
     return x
 
 
