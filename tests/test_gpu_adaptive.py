@@ -56,6 +56,12 @@ CASES = [
     (1, 4, 2, 400, 192, 40, False),
     (1, 2, 2, 350, 224, 35, False),
     (1, 8, 4, 333, 224, 34, True),
+    # contexts beyond the 8192-key sample: the selection ranks a window found
+    # from a sample of the keys (ties can overflow it: whole-head select)
+    (1, 4, 2, 20000, 128, 2000, True),
+    (1, 8, 2, 40000, 128, 4000, False),
+    (2, 4, 4, 12000, 64, 1, False),
+    (1, 2, 2, 9000, 256, 8999, False),
 ]
 
 
@@ -96,6 +102,26 @@ def test_adaptive_limits(F):
     c = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
     close(to_np(a0).astype(np.float32), to_np(b).astype(np.float32), rel=1e-3, what="k=0")
     close(to_np(aS).astype(np.float32), to_np(c).astype(np.float32), rel=1e-3, what="k=S")
+
+
+@pytest.mark.parametrize("S,k", [(10000, 1000), (3000, 300)])
+def test_adaptive_all_keys_tied(F, S, k):
+    """Every key of a head equal: one score, so the k keys of lowest index are
+    taken (beyond the sample size the window holds every key and overflows the
+    per-chunk lists: the whole-head select decides)."""
+    say(f"case adaptive all tied S={S}")
+    B, Hq, Hkv, d = 1, 4, 2, 128
+    q, kx, vx = make(B, Hq, Hkv, S, d, seed=21)
+    kx[:] = kx[:, :, :1, :]
+    kb, kr = F.encode_fused(torch.from_numpy(kx.reshape(-1, d)).cuda())
+    vb, vr = F.encode_fused(torch.from_numpy(vx.reshape(-1, d)).cuda())
+    _, sel = F.adaptive_attention(torch.from_numpy(q).cuda(), kb, kr, vb, vr, B, Hq, S, d,
+                                  n_kv_heads=Hkv, top_k=k, return_selected=True)
+    sel = to_np(sel)
+    want = np.zeros(S, bool)
+    want[:k] = True
+    for h in range(Hq):
+        assert np.array_equal(sel[0, h].astype(bool), want), f"head {h}"
 
 
 def test_config_c5_sample(F):
