@@ -215,24 +215,33 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         qint[i] = (int)__builtin_rintf(qf[i] / (qd.dq[i / D] * (1.0f / 256.0f)));
     __syncthreads();
     // digit j of the 8 elements of word w: nibble k = element 8w + k (balanced
-    // base 16: t = sum_j d_j 16^j, d_j in [-8, 7])
-    for (int e = tid; e < G * (D / 8) * 6; e += 256) {
-        const int j = e % 6, gw = e / 6, g = gw / (D / 8), w = gw % (D / 8);
-        uint32_t word = 0u;
+    // base 16: t = sum_j d_j 16^j, d_j in [-8, 7]).  Four threads per word
+    // (a DPP quad), two elements each; the quad ORs its nibbles together.
+    static_assert((G * D / 2) % 4 == 0, "whole quads per digit word");
+    for (int e = tid; e < G * (D / 2); e += 256) {
+        const int gw = e >> 2, q = e & 3, g = gw / (D / 8), w = gw % (D / 8);
+        uint32_t word[6];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
+        for (int j = 0; j < 6; j++) word[j] = 0u;
+#pragma unroll
+        for (int k = 2 * q; k < 2 * q + 2; k++) {
             int t = qint[g * D + 8 * w + k];
-            int d = 0;
 #pragma unroll
-            for (int jj = 0; jj < 6; jj++) {
-                d = ((t + 8) & 15) - 8;
-                if (jj == j) break;
+            for (int j = 0; j < 6; j++) {
+                const int d = ((t + 8) & 15) - 8;
+                word[j] |= ((uint32_t)d & 0xFu) << (4 * k);
                 t = (t - d) >> 4;
             }
-            word |= ((uint32_t)d & 0xFu) << (4 * k);
         }
-        if (j >= 2) ((int*)&qd.digits[g][w])[j - 2] = (int)word;
-        else ((int*)&qd.digits_lo[g][w])[j] = (int)word;
+#pragma unroll
+        for (int j = 0; j < 6; j++) {
+            word[j] |= dpp_u<0xB1>(word[j]);   // quad 1,0,3,2
+            word[j] |= dpp_u<0x4E>(word[j]);   // quad 2,3,0,1
+        }
+        if (q == 0) {
+            qd.digits[g][w] = make_int4((int)word[2], (int)word[3], (int)word[4], (int)word[5]);
+            qd.digits_lo[g][w] = make_int2((int)word[0], (int)word[1]);
+        }
     }
     if constexpr (KMF) {
         // B operand words, q_int = p0 + 256 p1 + 65536 p2 with p_i in

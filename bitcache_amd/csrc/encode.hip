@@ -376,7 +376,7 @@ __device__ __forceinline__ void encode_two_slices(const bc_v4u ra, const bc_v4u 
 // iteration (encode_two_slices), coalesced loads and stores, all reductions
 // on DPP / swizzle lane moves.  Same results as encode_kernel.
 template <int D, int MODE>
-__global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1) {
+__global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1, int run) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
     constexpr int L = D / 16;       // lanes per vector
     constexpr int VPW = 64 / L;     // vectors per wave
@@ -392,6 +392,9 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
 #pragma unroll 1
     for (int jb = 0; jb < 2; jb++) {
         const EncodeJob& J = jb ? j1 : j0;
+        // the second job starts at the other half of the waves (jobs of a
+        // few runs then run side by side)
+        const int64_t wid = jb ? (wave_id + nwaves / 2) % nwaves : wave_id;
         // (jobs hold fewer than 2^31 vectors: 32-bit vector indices)
         auto vec_of = [&](int64_t b) -> int64_t {
             return (int64_t)min((uint32_t)b + (uint32_t)sub, (uint32_t)J.n - 1u);
@@ -413,12 +416,12 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
             return dest_index(J, vec_of(b));
         };
         const EncodeDst dst{J.sign_plane, J.scale_plane, J.code_plane, J.rscale_plane};
-        // each wave encodes runs of kRun * VPW consecutive vectors, so that the
-        // cache lines of the scale and sign planes are written whole by one
-        // wave (one L2) rather than in pieces from several XCDs
-        constexpr int64_t kRun = 16;
+        // each wave encodes runs of `run` x VPW consecutive vectors (runs of 16
+        // write the cache lines of the scale and sign planes whole from one
+        // wave, i.e. one L2, rather than in pieces from several XCDs; small
+        // jobs take runs of 1 to spread over the waves)
         auto base_of = [&](int64_t t) {
-            return ((t / kRun) * nwaves + wave_id) * (kRun * VPW) + (t % kRun) * VPW;
+            return ((t / run) * nwaves + wid) * (run * VPW) + (t % run) * VPW;
         };
         // fp16 1.0 hidden from constant folding (see encode_two_slices)
         _Float16 one = (_Float16)1.0f;
@@ -472,7 +475,7 @@ constexpr int kEncodeBlocksPerCU = 3;
 // 256-thread blocks of `kernel` resident per CU (occupancy query, once per
 // kernel; at least 1)
 template <int MODE>
-int resident_blocks(int d, void (*kernel)(EncodeJob, EncodeJob)) {
+int resident_blocks(int d, void (*kernel)(EncodeJob, EncodeJob, int)) {
     static std::mutex mu;
     static int cached[3] = {0, 0, 0};
     const int slot = d == 64 ? 0 : (d == 128 ? 1 : 2);
@@ -488,19 +491,22 @@ int resident_blocks(int d, void (*kernel)(EncodeJob, EncodeJob)) {
 template <int MODE>
 int launch_encode(int d, const EncodeJob& a, const EncodeJob& b, hipStream_t st) {
     if (d == 64 || d == 128 || d == 256) {
-        // row encoder: 64/P vectors per wave, 4 waves per block, runs of 16
-        // wave iterations, grid-stride over at most kEncodeBlocksPerCU blocks
-        // per CU, all resident at once (a grid of several rounds ends with a
-        // round at low occupancy)
-        const int64_t vpb = 4 * (64 / (d / 16)) * 16;
-        const int64_t want = (a.n + b.n + vpb - 1) / vpb;
+        // row encoder: 64/P vectors per wave, 4 waves per block, grid-stride
+        // over at most kEncodeBlocksPerCU blocks per CU, all resident at once
+        // (a grid of several rounds ends with a round at low occupancy)
         auto kernel = d == 64 ? encode_rows_kernel<64, MODE>
                               : (d == 128 ? encode_rows_kernel<128, MODE> : encode_rows_kernel<256, MODE>);
         const int per_cu = resident_blocks<MODE>(d, kernel);
         const int64_t cap =
             (int64_t)bc::device_cu_count() * (per_cu < kEncodeBlocksPerCU ? per_cu : kEncodeBlocksPerCU);
-        const int grid = (int)(want < cap ? (want < 1 ? 1 : want) : cap);
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, a, b);
+        // a grid of one iteration per wave if that fits, else the resident
+        // blocks with runs of up to 16 iterations (a quarter of each wave's)
+        const int64_t vpw = 64 / (d / 16);
+        const int64_t one_pass = (a.n + b.n + 4 * vpw - 1) / (4 * vpw);
+        const int grid = (int)(one_pass < cap ? (one_pass < 1 ? 1 : one_pass) : cap);
+        const int64_t per_wave = (a.n + b.n + (int64_t)grid * 4 * vpw - 1) / ((int64_t)grid * 4 * vpw);
+        const int run = (int)(per_wave / 4 < 1 ? 1 : (per_wave / 4 > 16 ? 16 : per_wave / 4));
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, a, b, run);
         return bc::check_launch("encode");
     }
     if constexpr (MODE == ENC_TRAFFIC) {
