@@ -376,7 +376,7 @@ __device__ __forceinline__ void encode_two_slices(const bc_v4u ra, const bc_v4u 
 // iteration (encode_two_slices), coalesced loads and stores, all reductions
 // on DPP / swizzle lane moves.  Same results as encode_kernel.
 template <int D, int MODE>
-__global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1, int run) {
+__global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJob j1, int lg_run) {
     static_assert(D == 64 || D == 128 || D == 256, "row encoder: d in {64, 128, 256}");
     constexpr int L = D / 16;       // lanes per vector
     constexpr int VPW = 64 / L;     // vectors per wave
@@ -394,7 +394,11 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
         const EncodeJob& J = jb ? j1 : j0;
         // the second job starts at the other half of the waves (jobs of a
         // few runs then run side by side)
-        const int64_t wid = jb ? (wave_id + nwaves / 2) % nwaves : wave_id;
+        int64_t wid = wave_id;
+        if (jb) {
+            wid += nwaves / 2;
+            if (wid >= nwaves) wid -= nwaves;
+        }
         // (jobs hold fewer than 2^31 vectors: 32-bit vector indices)
         auto vec_of = [&](int64_t b) -> int64_t {
             return (int64_t)min((uint32_t)b + (uint32_t)sub, (uint32_t)J.n - 1u);
@@ -416,12 +420,20 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
             return dest_index(J, vec_of(b));
         };
         const EncodeDst dst{J.sign_plane, J.scale_plane, J.code_plane, J.rscale_plane};
-        // each wave encodes runs of `run` x VPW consecutive vectors (runs of 16
-        // write the cache lines of the scale and sign planes whole from one
-        // wave, i.e. one L2, rather than in pieces from several XCDs; small
-        // jobs take runs of 1 to spread over the waves)
-        auto base_of = [&](int64_t t) {
-            return ((t / run) * nwaves + wid) * (run * VPW) + (t % run) * VPW;
+        // each wave encodes runs of 2^lg_run x VPW consecutive vectors (runs
+        // of 16 write the cache lines of the scale and sign planes whole from
+        // one wave, i.e. one L2, rather than in pieces from several XCDs;
+        // small jobs take runs of 1 to spread over the waves).  Iteration t of
+        // the wave starts at ((t >> lg) nwaves + wid) VPW 2^lg + (t mod 2^lg) VPW,
+        // stepped incrementally: +VPW inside a run, +jump to the next run.
+        const int run = 1 << lg_run;
+        const int64_t jump = (int64_t)VPW + (nwaves - 1) * ((int64_t)run * VPW);
+        auto step = [&](int64_t b, int& pos) -> int64_t {
+            if (++pos == run) {
+                pos = 0;
+                return b + jump;
+            }
+            return b + VPW;
         };
         // fp16 1.0 hidden from constant folding (see encode_two_slices)
         _Float16 one = (_Float16)1.0f;
@@ -437,25 +449,24 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(EncodeJob j0, EncodeJo
         // the load in flight); the prefetch is issued unconditionally (past
         // the last iteration it reloads the current slices) so that the wait
         // before each encode leaves it in flight
-        int64_t t = 0;
-        int64_t base = base_of(0);
+        int64_t base = wid * ((int64_t)run * VPW);
         if (base >= J.n) continue;
+        int pos = 0;   // (wave-uniform: base, pos and nb run on scalar registers)
         bc_v4u ra, rb, qa, qb;
         load(base, ra, rb);
         for (;;) {
-            int64_t nb = base_of(t + 1);
-            bool more = nb < J.n;   // (wave-uniform)
+            int64_t nb = step(base, pos);
+            bool more = nb < J.n;
             load(more ? nb : base, qa, qb);
             encode_two_slices<D, MODE>(ra, rb, j, base + sub < J.n, dst, dest_for(base), one);
             if (!more) break;
             base = nb;
-            nb = base_of(t + 2);
+            nb = step(base, pos);
             more = nb < J.n;
             load(more ? nb : base, ra, rb);
             encode_two_slices<D, MODE>(qa, qb, j, base + sub < J.n, dst, dest_for(base), one);
             if (!more) break;
             base = nb;
-            t += 2;
         }
     }
 }
@@ -500,13 +511,15 @@ int launch_encode(int d, const EncodeJob& a, const EncodeJob& b, hipStream_t st)
         const int64_t cap =
             (int64_t)bc::device_cu_count() * (per_cu < kEncodeBlocksPerCU ? per_cu : kEncodeBlocksPerCU);
         // a grid of one iteration per wave if that fits, else the resident
-        // blocks with runs of up to 16 iterations (a quarter of each wave's)
+        // blocks with runs of up to 16 iterations (at most a quarter of each
+        // wave's, a power of two)
         const int64_t vpw = 64 / (d / 16);
         const int64_t one_pass = (a.n + b.n + 4 * vpw - 1) / (4 * vpw);
         const int grid = (int)(one_pass < cap ? (one_pass < 1 ? 1 : one_pass) : cap);
         const int64_t per_wave = (a.n + b.n + (int64_t)grid * 4 * vpw - 1) / ((int64_t)grid * 4 * vpw);
-        const int run = (int)(per_wave / 4 < 1 ? 1 : (per_wave / 4 > 16 ? 16 : per_wave / 4));
-        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, a, b, run);
+        int lg_run = 0;
+        while (lg_run < 4 && (int64_t)(2 << lg_run) * 4 <= per_wave) lg_run++;
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, a, b, lg_run);
         return bc::check_launch("encode");
     }
     if constexpr (MODE == ENC_TRAFFIC) {
