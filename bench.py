@@ -46,11 +46,11 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profiles():
-    """HBM bytes per launch of the split kernel from the committed rocprofv3
-    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
-    or None if no summary is present."""
-    path = os.path.join(ROOT, "profiles", "attn_mfma_kernel_c3_counters.md")
+def traffic_from_profiles(name="attn_mfma_kernel_c3_counters.md"):
+    """HBM bytes per launch of a kernel from its committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factors), or
+    None if no summary is present."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
@@ -338,7 +338,8 @@ def bench_prefill(args, torch, _C, W):
                                "c3 K or V tensor; head entropy over the encoded K",
                    "vectors": n, "head_dim": d, "bytes_per_tensor": alg},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_profiles("encode_rows_kernel_prefill_counters.md"),
                      "kernel": "encode_rows_kernel<128, fused fp16 scale>"},
         "traffic_floor_us": round(floor_ms * 1e3, 1),
         "traffic_floor_gbps": round(alg / (floor_ms * 1e-3) / 1e9, 1),

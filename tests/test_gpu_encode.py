@@ -259,3 +259,21 @@ def test_encode_prefill_scale_property(F):
     assert np.array_equal(gb.words[idx], eb.words)
     assert np.array_equal(gb.scale[idx].view(np.uint16), eb.scale.view(np.uint16))
     assert np.array_equal(gr.codes[idx], er.codes)
+
+
+@pytest.mark.parametrize("d,n", [(64, 5000), (128, 3001), (256, 777)])
+def test_traffic_probe_stays_in_its_blobs(d, n):
+    """The encoder's traffic probe (same loads and stores, no arithmetic)
+    writes only inside the two blobs it is given: guard bytes after each blob
+    keep their value, and the source is not modified."""
+    from bitcache_amd import _C
+    say(f"case traffic_probe d={d} n={n}")
+    x = torch.from_numpy(rand_x(n, d, 7)).cuda()
+    x0 = x.clone()
+    guard = 4096
+    bfull = torch.full((n * 36 + guard,), 0xA5, dtype=torch.uint8, device="cuda")
+    rfull = torch.full((n * 130 + guard,), 0x5A, dtype=torch.uint8, device="cuda")
+    _C.encode_traffic_probe(x, bfull[:n * 36], rfull[:n * 130])
+    torch.cuda.synchronize()
+    assert torch.all(bfull[n * 36:] == 0xA5) and torch.all(rfull[n * 130:] == 0x5A)
+    assert torch.equal(x.view(torch.int16), x0.view(torch.int16))   # bitwise (x holds a NaN)
