@@ -46,14 +46,14 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profiles(name="attn_mfma_kernel_c3_counters.md"):
-    """HBM bytes per launch of a kernel from its committed rocprofv3 --pmc
+def traffic_from_profiles(name="attn_mfma_kernel_c3_counters.md", key="traffic_bytes_per_launch"):
+    """HBM bytes per launch (or per step) from a committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factors), or
     None if no summary is present."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    m = re.search(key + r":\s*([0-9.eE+]+)", open(path).read())
     return float(m.group(1)) if m else None
 
 
@@ -192,7 +192,8 @@ def bench_c2(args, torch, _C, W):
                    "batch": B, "heads": H, "seq_len": S, "head_dim": d, "bytes_per_step": alg},
         "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "kernel": "attention step (split + combine), wall clock"},
+                     "traffic": traffic_from_profiles("traffic_c2_c5_counters.md", "traffic_bytes_per_step_c2"),
+                     "kernel": "attention step (split + combine), wall clock"},
         "kendall_tau": {"vs": "exact q.k (fp32) per (b, h), all 32768 keys",
                         "tau_a_mean": round(sum(ta) / len(ta), 4), "tau_a_min": round(min(ta), 4),
                         "tau_b_mean": round(sum(tb) / len(tb), 4), "tau_b_min": round(min(tb), 4),
@@ -294,7 +295,8 @@ def bench_c5(args, torch, _C, W):
                    "batch": B, "heads": Hq, "kv_heads": Hkv, "seq_len": S, "head_dim": d,
                    "top_k": top_k, "residual_keys_read": n_res, "bytes_per_step": alg},
         "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_profiles("traffic_c2_c5_counters.md", "traffic_bytes_per_step_c5"),
                      "kernel": "whole adaptive step (radix passes + attention), wall clock"},
         "full_compensated_us": round(wall_c * 1e6, 1),
     }
