@@ -180,27 +180,42 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
     static_assert((G * D) % 64 == 0, "whole waves of query elements");
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t* signs = &qd.signs[0][0];   // [G * D / 32] words, bit b of word i = element 32i + b
+    __shared__ float gmax[G * D / 64];   // max |q| of each 64-element group
+    // the three int8 planes of q_int per element (int8 MFMA operands)
+    __shared__ __attribute__((aligned(8))) uint8_t pbytes[KMF ? 3 : 1][KMF ? G * D : 8];
+    // floats, sign words (wave ballots) and each wave's max |q| (its 64
+    // elements lie in one head)
     for (int i = tid; i < G * D; i += 256) {
         const float x = h2f(qbase[i]);
         qf[i] = x;
         const uint64_t bits = __ballot(x >= 0.0f);
+        const float wm = wave_max(fabsf(x));
         if (lane == 0) {
             signs[i / 32] = (uint32_t)bits;
             signs[i / 32 + 1] = (uint32_t)(bits >> 32);
+            gmax[i / 64] = wm;
         }
     }
     __syncthreads();
     if (tid < G) {
-        // sequential fp32 order (element 0 first); the reads are independent
-        float acc = 0.0f, mx = 0.0f;
+        // sequential fp32 order (element 0 first), eight float4 reads in
+        // flight at a time
+        float acc = 0.0f;
         const float4* q4 = (const float4*)&qf[tid * D];
 #pragma unroll
-        for (int c = 0; c < D / 4; c++) {
-            const float4 v = q4[c];
-            acc += fabsf(v.x); acc += fabsf(v.y); acc += fabsf(v.z); acc += fabsf(v.w);
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        for (int c0 = 0; c0 < D / 4; c0 += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = q4[c0 + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc += fabsf(v[u].x); acc += fabsf(v[u].y); acc += fabsf(v[u].z); acc += fabsf(v[u].w);
+            }
         }
         qd.scale_q[tid] = acc / (float)D;
+        float mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < D / 64; k++) mx = fmaxf(mx, gmax[tid * (D / 64) + k]);
         qd.dq[tid] = mx > 0.0f ? 256.0f * (mx / kQIntMax) : 256.0f;
     }
     __syncthreads();
@@ -209,10 +224,21 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         for (int g = 0; g < G; g++) m = fmaxf(m, qd.dq[g]);
         qd.prec_bound = 0.53f * m * sqrtf((float)D);
     }
-    // q_int over the floats: each thread converts the elements it reads
+    // q_int over the floats (each thread converts the elements it reads) and
+    // its balanced int8 planes, q_int = p0 + 256 p1 + 65536 p2, p_i in [-128, 127]
     int* qint = (int*)qf;
-    for (int i = tid; i < G * D; i += 256)
-        qint[i] = (int)__builtin_rintf(qf[i] / (qd.dq[i / D] * (1.0f / 256.0f)));
+    for (int i = tid; i < G * D; i += 256) {
+        const int t = (int)__builtin_rintf(qf[i] / (qd.dq[i / D] * (1.0f / 256.0f)));
+        qint[i] = t;
+        if constexpr (KMF) {
+            const int p0 = ((t + 128) & 255) - 128;
+            const int t1 = (t - p0) >> 8;
+            const int p1 = ((t1 + 128) & 255) - 128;
+            pbytes[0][i] = (uint8_t)p0;
+            pbytes[1][i] = (uint8_t)p1;
+            pbytes[2][i] = (uint8_t)((t1 - p1) >> 8);
+        }
+    }
     __syncthreads();
     // digit j of the 8 elements of word w: nibble k = element 8w + k (balanced
     // base 16: t = sum_j d_j 16^j, d_j in [-8, 7]).  Four threads per word
@@ -244,43 +270,40 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         }
     }
     if constexpr (KMF) {
-        // B operand words, q_int = p0 + 256 p1 + 65536 p2 with p_i in
-        // [-128, 127]: column c = 2g + p (c < 2G) holds plane p + 1 of head g,
-        // column 2G + g plane 0 of head g when 3G <= 16 (bq_lo column 2g
-        // otherwise); slot s = 4r + j of lane group q for piece pc and half h
-        // holds dim 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the unpacked
-        // codes put it
+        // B operand words: column c = 2g + p (c < 2G) holds plane p + 1 of
+        // head g, column 2G + g plane 0 of head g when 3G <= 16 (bq_lo column
+        // 2g otherwise); slot s = 4r + j of lane group q for piece pc and half
+        // h holds dim 32 (q + 4 pc) + 8 (2h + r/2) + 2j + r%2, where the
+        // unpacked codes put it: words r = 2rr, 2rr + 1 are the even and odd
+        // bytes of the 8 plane bytes at dim 32 (q + 4 pc) + 8 (2h + rr)
         constexpr int NPC = D / 128;
         constexpr bool LO_COLS = 3 * G <= 16;
         for (int e = tid; e < NPC * 2 * 64; e += 256) {
             const int pc = e / 128, h = (e / 64) & 1, ln = e & 63;
             const int col = ln & 15, qg4 = ln >> 4;
-            int wd[4], wl[4];
-            for (int r = 0; r < 4; r++) {
-                uint32_t word = 0, wlo = 0;
-                for (int j = 0; j < 4; j++) {
-                    const int dim = 32 * (qg4 + 4 * pc) + 8 * (2 * h + (r >> 1)) + 2 * j + (r & 1);
-                    auto planes = [&](int g, int& p0, int& p1, int& p2) {
-                        const int t = qint[g * D + dim];
-                        p0 = ((t + 128) & 255) - 128;
-                        const int t1 = (t - p0) >> 8;
-                        p1 = ((t1 + 128) & 255) - 128;
-                        p2 = (t1 - p1) >> 8;
-                    };
-                    int p0, p1, p2, v = 0, vl = 0;
-                    if (col < 2 * G) {
-                        planes(col >> 1, p0, p1, p2);
-                        v = (col & 1) ? p2 : p1;
-                        if (!LO_COLS && !(col & 1)) vl = p0;
-                    } else if (LO_COLS && col < 3 * G) {
-                        planes(col - 2 * G, p0, p1, p2);
-                        v = p0;
-                    }
-                    word |= ((uint32_t)v & 0xFFu) << (8 * j);
-                    wlo |= ((uint32_t)vl & 0xFFu) << (8 * j);
+            int gv = 0, pv = -1;   // the lane's column: plane pv of head gv (pv < 0: zeros)
+            if (col < 2 * G) {
+                gv = col >> 1;
+                pv = (col & 1) ? 2 : 1;
+            } else if (LO_COLS && col < 3 * G) {
+                gv = col - 2 * G;
+                pv = 0;
+            }
+            const bool lo_col = !LO_COLS && col < 2 * G && !(col & 1);
+            int wd[4] = {0, 0, 0, 0}, wl[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int rr = 0; rr < 2; rr++) {
+                const int at = gv * D + 32 * (qg4 + 4 * pc) + 8 * (2 * h + rr);
+                if (pv >= 0) {
+                    const bc_v2u x = *(const bc_v2u*)&pbytes[pv][at];
+                    wd[2 * rr] = (int)__builtin_amdgcn_perm(x[1], x[0], 0x06040200u);
+                    wd[2 * rr + 1] = (int)__builtin_amdgcn_perm(x[1], x[0], 0x07050301u);
                 }
-                wd[r] = (int)word;
-                wl[r] = (int)wlo;
+                if (lo_col) {
+                    const bc_v2u x = *(const bc_v2u*)&pbytes[0][at];
+                    wl[2 * rr] = (int)__builtin_amdgcn_perm(x[1], x[0], 0x06040200u);
+                    wl[2 * rr + 1] = (int)__builtin_amdgcn_perm(x[1], x[0], 0x07050301u);
+                }
             }
             qd.bq[pc][h][ln] = make_int4(wd[0], wd[1], wd[2], wd[3]);
             if constexpr (!LO_COLS) qd.bq_lo[pc][h][ln] = make_int4(wl[0], wl[1], wl[2], wl[3]);
