@@ -159,6 +159,15 @@ __device__ __forceinline__ int slot_of(int k) {
     return 16 * g4 + 8 * mh + ((r & 3) << 1) + (r >> 2);
 }
 
+// Slot of key k in the int8 weight columns: the 16 K-slots of lane group g4
+// in the 16x16x64 int8 MFMA are the keys of that group's transposed sign
+// read in register order, i.e. even then odd nibbles of its first word
+// (keys 16g4 + 0..7), then of its second (keys 16g4 + 8..15).
+__device__ __forceinline__ int slot8_of(int k) {
+    const int g4 = k >> 4, hw = (k >> 3) & 1, r = k & 7;
+    return 16 * g4 + 8 * hw + 4 * (r & 1) + (r >> 1);
+}
+
 // Adaptive mode packs the keys of a tile that some head selected into
 // positions 0..n-1 of its residual data.  Position j sits in V staging row
 // res_row(j): rows 16g + 0..7 feed MFMA half 0 and rows 16g + 8..15 half 1, so
@@ -413,12 +422,24 @@ void attn_mfma_kernel(AttnArgs a) {
     // per CU (measured faster); adaptive mode keeps it
     constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || (MODE == MODE_ADAPTIVE && BC_ADAPT_PIPE) || BC_GQA_PIPE;
     using WL = WaveLds<D, G, RES>;
+    // Binary mode, groups up to 4: the value MFMAs run on int8 operands.  The
+    // sign bits enter in place (element 2^p for bit p of a nibble, four keys
+    // per AND instead of two fp16 elements) and each weight as a 22-bit
+    // integer in three balanced 8-bit digit columns (columns 4g + plane, the
+    // fourth unused), summed exactly in int32 accumulators that the online
+    // softmax rescales by powers of two (integer reference m).
+    constexpr bool I8 = MODE == MODE_BINARY && G <= 4;
+    constexpr int kW8Stride = 80;   // bytes per int8 weight column (64 slots + pad)
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
     __shared__ __attribute__((aligned(16))) uint8_t lds_st0[4][WL::kStage];
     __shared__ __attribute__((aligned(16))) uint8_t lds_st1[4][PIPE ? WL::kStage : 16];
-    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][WL::kWeightBytes / 2];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][I8 ? 8 : WL::kWeightBytes / 2];
+    __shared__ __attribute__((aligned(16))) int8_t lds_w8[4][I8 ? 4 * G * kW8Stride : 16];
+    // (int8 path) per wave and head, the float sums of the keys before the
+    // last rescale, [head][D] in the epilogue's dim order
+    __shared__ __attribute__((aligned(16))) float lds_bank[4][I8 ? G * D : 4];
     __shared__ __attribute__((aligned(16))) int lds_rd[4][WL::kRdInts];
     __shared__ __attribute__((aligned(16))) int lds_rdlo[4][(KMF && 3 * G <= 16) ? WL::kRdInts : 1];
     __shared__ float wofs[4][G];
@@ -481,7 +502,7 @@ void attn_mfma_kernel(AttnArgs a) {
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
-    const int my_head = my_col >> 1;
+    const int my_head = I8 ? my_col >> 2 : my_col >> 1;
     const int bcol = my_col < 2 * G ? my_col : (my_col & 1);
 
     // weight columns [2 parts][2G cols][72 slots]: this lane's store slot in
@@ -491,13 +512,20 @@ void attn_mfma_kernel(AttnArgs a) {
     // tie to one array wait for all direct loads in flight, the prefetch too)
     uint16_t* wsl = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + slot_of(kown));
     const uint16_t* wrd = &lds_wts[0][0] + opaque_int(wave * (WL::kWeightBytes / 2) + bcol * WL::kColSlots + 16 * g4);
+    // int8 weight columns [4G cols][80 bytes]: this lane's digit bytes at its
+    // key's slot of column 0, and its B-operand read (16 bytes of column
+    // my_col; lanes of unused columns read column 0 again)
+    int8_t* w8st = &lds_w8[0][0] + opaque_int(wave * (I8 ? 4 * G * kW8Stride : 16) + (I8 ? slot8_of(kown) : 0));
+    const int8_t* w8rd = &lds_w8[0][0] + opaque_int(wave * (I8 ? 4 * G * kW8Stride : 16) +
+                                                    (I8 ? (my_col < 4 * G ? my_col : 0) * kW8Stride + 16 * g4 : 0));
     int* rdl = lds_rd[wave];          // [64 keys][G] residual dots
     int* rdlo = lds_rdlo[wave];       // their plane-0 parts (precise tiles)
 
     // softmax reference per head, lowered lazily: weights p = 2^(s - m) stay
     // <= 2^kTau, and the accumulators are rescaled only when a score passes
-    // m + kTau (the result does not depend on m)
-    constexpr int kTauI = 8;
+    // m + kTau (the result does not depend on m).  The int8 path's fixed-point
+    // weights give up kTau of their 22 bits to this headroom: 4 there.
+    constexpr int kTauI = I8 ? 4 : 8;
     constexpr float kTau = (float)kTauI;
     float m[G], mlim[G], lsum[G], off[G];
 #pragma unroll
@@ -507,19 +535,53 @@ void attn_mfma_kernel(AttnArgs a) {
         lsum[g] = 0.0f;
         off[g] = 0.0f;
     }
-    f4_t cs[NH][4];   // sign part: [block][p] rows = dims 64h + 4m + p
+    f4_t cs[I8 ? 1 : NH][4];   // sign part: [block][p] rows = dims 64h + 4m + p
+    v4i_t ci[I8 ? NH : 1][4];  // (int8 path) the same, per digit column
     f4_t cn[NB];      // residual part: rows = dims 16db + m
 #pragma unroll
-    for (int h = 0; h < NH; h++)
+    for (int h = 0; h < (I8 ? 1 : NH); h++)
 #pragma unroll
         for (int p = 0; p < 4; p++) cs[h][p] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
+    for (int h = 0; h < (I8 ? NH : 1); h++)
+#pragma unroll
+        for (int p = 0; p < 4; p++) ci[h][p] = v4i_t{0, 0, 0, 0};
+#pragma unroll
     for (int d = 0; d < NB; d++) cn[d] = f4_t{0.f, 0.f, 0.f, 0.f};
 
+    // (int8 path) a head's digit columns 4g + 0..2 are one lane quad; its
+    // first lane owns the head's rows in the bank.  flush8: bank = (bank +
+    // d0 + 256 d1 + 65536 d2) * f per element, the integer sums restart at 0
+    const bool owner8 = I8 && my_col < 4 * G && (my_col & 3) == 0;
+    float* bank = &lds_bank[0][0] + opaque_int(wave * (I8 ? G * D : 4) + (I8 ? (my_col >> 2) * D : 0));
+    bool banked = false;   // (wave-uniform) the bank holds values
+    bool live8 = false;    // (wave-uniform) the integer sums hold values
+    auto flush8 = [&](float f) {
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float t[4];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const float v0 = (float)ci[h][p][i];
+                    t[p] = v0 + 256.0f * dpp_f<0x39>(v0) + 65536.0f * dpp_f<0x4E>(v0);
+                    ci[h][p][i] = 0;
+                }
+                if (owner8) {
+                    float4* bp = (float4*)&bank[64 * h + 4 * (4 * g4 + i)];
+                    float4 b = banked ? *bp : make_float4(0.f, 0.f, 0.f, 0.f);
+                    *bp = make_float4((b.x + t[0]) * f, (b.y + t[1]) * f, (b.z + t[2]) * f, (b.w + t[3]) * f);
+                }
+            }
+        banked = true;
+    };
+
     // weights enter the MFMAs as w * 2^wexp (fp16 hi + lo), wexp chosen so the
-    // largest possible weight sits near 2^14: no overflow, and weights down to
-    // ~2^-30 of the largest keep their contribution (undone exactly in the
-    // epilogue)
+    // largest possible weight sits near 2^14 (int8 path: integers up to 2^22):
+    // no overflow, and weights down to ~2^-30 of the largest keep their
+    // contribution (fp16; undone exactly in the epilogue)
+    constexpr int kWTop = I8 ? 22 : 14;
     int wexp = 0;
     bool have_wexp = false;
     float wlim = 0.0f;
@@ -1038,21 +1100,26 @@ void attn_mfma_kernel(AttnArgs a) {
         }
 
         // weight scale: weights are p * wb * 2^wexp with p <= 2^kTau, so the
-        // plan holds while every wb <= wlim = 2^(14 - kTau - wexp); it is redone
-        // (one wave max) only when a key exceeds it, and then only lowered
+        // plan holds while every wb <= wlim = 2^(kWTop - kTau - wexp); it is
+        // redone (one wave max) only when a key exceeds it, and then only lowered
+        float wfac = 1.0f;   // (int8 path) the factor that lowering applies
         {
             const float wb = valid ? fmaxf(2.0f * svv, rsv * (1.0f / 7.0f)) : 0.0f;
             if (__ballot(wb > wlim) != 0ull) {
                 const float wmx = wave_max(wb);
                 if (wmx < INFINITY) {
-                    const int e = 14 - kTauI - (int)ceilf(log2f(wmx));
+                    const int e = kWTop - kTauI - (int)ceilf(log2f(wmx));
                     if (have_wexp) {
                         // a larger weight than planned (e < wexp): bring the sums down
                         const float f = ldexpf(1.0f, e - wexp);
+                        if constexpr (I8) {
+                            wfac = f;   // applied by the flush below
+                        } else {
 #pragma unroll
-                        for (int h = 0; h < NH; h++)
+                            for (int h = 0; h < NH; h++)
 #pragma unroll
-                            for (int p = 0; p < 4; p++) cs[h][p] *= f;
+                                for (int p = 0; p < 4; p++) cs[h][p] *= f;
+                        }
 #pragma unroll
                         for (int d = 0; d < NB; d++) cn[d] *= f;
 #pragma unroll
@@ -1060,7 +1127,7 @@ void attn_mfma_kernel(AttnArgs a) {
                     }
                     wexp = e;
                     have_wexp = true;
-                    wlim = ldexpf(1.0f, 14 - kTauI - wexp);
+                    wlim = ldexpf(1.0f, kWTop - kTauI - wexp);
                 }
             }
         }
@@ -1071,8 +1138,8 @@ void attn_mfma_kernel(AttnArgs a) {
         // the value operands of odd rows come out 16x larger (see the MFMA
         // loops below): their weights carry 1/16 so that every product is exact
         // (the residual row of a key is its compacted position's row, of the
-        // parity of rpos)
-        const float kfac = (kown & 1) ? 0.0625f : 1.0f;
+        // parity of rpos); the int8 sign elements carry no such factor
+        const float kfac = (!I8 && (kown & 1)) ? 0.0625f : 1.0f;
         const float kfac_res = (rpos & 1) ? 0.0625f : 1.0f;
         // per-key factors shared by the heads: sign weight a2 = p * fa, residual
         // weight b = p * fb, and the offset sum_s (a_s + 8 b_s) grows by p * fo
@@ -1116,21 +1183,41 @@ void attn_mfma_kernel(AttnArgs a) {
                 bv = selg ? p * fb : 0.0f;
                 fo = selg ? fo_res : fo_bin;
             }
-            const uint16_t a2h = f2h_bits(a2);
-            const uint16_t a2l = f2h_bits(a2 - h_bits2f(a2h));
-            const uint16_t bh = f2h_bits(bv);
-            const uint16_t bl = f2h_bits(bv - h_bits2f(bh));
             // offset removed at the end, from the unrounded weights: the (hi, lo)
-            // pairs carry ~22 bits, so the difference is a zero-mean ~2^-22 term
+            // pairs carry ~22 bits (int8 path: rounding to integers up to
+            // 2^22), so the difference is a zero-mean ~2^-22 term
             off[g] = fmaf(p, fo, off[g]);
-            wsl[(0 * 2 * G + 2 * g) * WL::kColSlots] = a2h;
-            wsl[(0 * 2 * G + 2 * g + 1) * WL::kColSlots] = a2l;
+            if constexpr (I8) {
+                // w = rint(a2) <= 2^22 from the low mantissa bits of
+                // a2 + 1.5 * 2^23, as balanced digits d0 + 256 d1 + 65536 d2:
+                // the bytes of w, of (w + 128) >> 8 and of (w + 32896) >> 16
+                const uint32_t wb3 = __builtin_bit_cast(uint32_t, a2 + 12582912.0f);
+                int8_t* ws = w8st + 4 * g * kW8Stride;
+                ws[0] = (int8_t)wb3;
+                ws[kW8Stride] = (int8_t)((wb3 + 128u) >> 8);
+                ws[2 * kW8Stride] = (int8_t)((wb3 - 4161408u) >> 16);   // (0x4B400000 - 0x400000 + 32896)
+            } else {
+                const uint16_t a2h = f2h_bits(a2);
+                const uint16_t a2l = f2h_bits(a2 - h_bits2f(a2h));
+                wsl[(0 * 2 * G + 2 * g) * WL::kColSlots] = a2h;
+                wsl[(0 * 2 * G + 2 * g + 1) * WL::kColSlots] = a2l;
+            }
             if constexpr (RES) {
+                const uint16_t bh = f2h_bits(bv);
+                const uint16_t bl = f2h_bits(bv - h_bits2f(bh));
                 wres[(1 * 2 * G + 2 * g) * WL::kColSlots] = bh;
                 wres[(1 * 2 * G + 2 * g + 1) * WL::kColSlots] = bl;
             }
         }
-        if (any_rescale) {
+        if constexpr (I8) {
+            // the integer sums so far move to the float bank, scaled by this
+            // tile's factors (rare: the weight plan was lowered or a score
+            // passed m + kTau)
+            if (live8 && (any_rescale || wfac != 1.0f)) {
+                if (my_head >= G) lane_alpha = 1.0f;
+                flush8(lane_alpha * wfac);
+            }
+        } else if (any_rescale) {
             if (my_head >= G) lane_alpha = 1.0f;
 #pragma unroll
             for (int h = 0; h < NH; h++)
@@ -1157,11 +1244,16 @@ void attn_mfma_kernel(AttnArgs a) {
         // B operands: (hi, lo) weight columns; lanes of unused columns read
         // columns 0/1 again (their output columns are never read back)
         h8_t bsig[2], bres[2];
+        v4i_t b8 = v4i_t{0, 0, 0, 0};
+        if constexpr (I8) {
+            b8 = *(const v4i_t*)w8rd;
+        } else {
 #pragma unroll
-        for (int mh = 0; mh < 2; mh++) {
-            bsig[mh] = *(const h8_t*)&wrd[(0 * 2 * G) * WL::kColSlots + 8 * mh];
-            if constexpr (RES) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * WL::kColSlots + 8 * mh];
-            else bres[mh] = bsig[mh];
+            for (int mh = 0; mh < 2; mh++) {
+                bsig[mh] = *(const h8_t*)&wrd[(0 * 2 * G) * WL::kColSlots + 8 * mh];
+                if constexpr (RES) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * WL::kColSlots + 8 * mh];
+                else bres[mh] = bsig[mh];
+            }
         }
 
         // all transposed reads of the tile first (they retire in order while
@@ -1186,8 +1278,26 @@ void attn_mfma_kernel(AttnArgs a) {
         }
 
         // sign part: rows = dims 64h + 4*lj + p
+        if constexpr (I8) {
+            // int8: the lane's 16 keys (first word keys 0..7, second 8..15,
+            // nibble r = key r) as bytes holding bit p of their nibble in
+            // place (element 2^p): even nibbles from the word, odd ones from
+            // the word >> 4, one AND per four keys; all 64 keys in one MFMA
 #pragma unroll
-        for (int h = 0; h < NH; h++) {
+            for (int h = 0; h < NH; h++) {
+                const uint32_t x = (uint32_t)wsg[h].x, y = (uint32_t)wsg[h].y;
+                const uint32_t x4 = x >> 4, y4 = y >> 4;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const uint32_t msk = 0x01010101u << p;
+                    const v4i_t av = v4i_t{(int)(x & msk), (int)(x4 & msk), (int)(y & msk), (int)(y4 & msk)};
+                    ci[h][p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b8, ci[h][p], 0, 0, 0);
+                }
+            }
+            live8 = true;
+        }
+#pragma unroll
+        for (int h = 0; h < (I8 ? 0 : NH); h++) {
 #pragma unroll
             for (int mh = 0; mh < 2; mh++) {
                 // x holds nibble r of key r (r = 0..3) and of key r + 4 (bits
@@ -1319,7 +1429,7 @@ void attn_mfma_kernel(AttnArgs a) {
         __builtin_amdgcn_wave_barrier();
     }
 
-    // ---------------- epilogue: per wave, per head: acc[e] = ((cs + cn) * 2^24 - off) * 2^-wexp,
+    // ---------------- epilogue: per wave, per head: acc[e] = ((cs + cn) * unit - off) * 2^-wexp,
     // then the four waves' partials are merged.  Heads pass through staging
     // buffer 0 kEpiHeads at a time ([parts][kEpiHeads][D] floats per wave).
     constexpr int HP = WL::kEpiHeads;
@@ -1355,24 +1465,57 @@ void attn_mfma_kernel(AttnArgs a) {
         hsum[1][g] = lv;
     }
     float* accw = (float*)lds_st0[wave];
-    // hi + lo columns are adjacent lanes (col 2g, 2g+1); the even lane writes
-    const bool writer = my_col < 2 * G && (my_col & 1) == 0;
+    // hi + lo columns are adjacent lanes (col 2g, 2g+1); the even lane writes.
+    // int8 path: the digit columns 4g + 0..2 of a head are one lane quad; its
+    // first lane writes
+    const bool writer = I8 ? (my_col < 4 * G && (my_col & 3) == 0) : (my_col < 2 * G && (my_col & 1) == 0);
+    // the sign part's unit: 2^-24 (fp16 subnormal elements) or 1 (int8)
+    const float sunit = I8 ? 1.0f : two24;
     for (int g0 = 0; g0 < G; g0 += HP) {
         const int hs = my_head - g0;   // this lane's head slot in the batch
         const bool wr = writer && hs >= 0 && hs < HP;
         if (g0 > 0) __syncthreads();   // the previous batch has been read
         // hi + lo: the neighbour lane's column by DPP (quad_perm [1,0,3,2]),
         // all sums first, then the stores under one branch
-        float sv[NH][4][4];
+        float sv[I8 ? 1 : NH][4][4];
         float nv[RES ? NB : 1][4];
+        if constexpr (I8) {
+            // digits d0 + 256 d1 + 65536 d2 from lanes +0, +1, +2 of the quad
+            // (quad_perm [1,2,3,0] and [2,3,0,1]); one 64-dim block at a time
+            // (accumulator p carries 2^p: bit p read in place)
 #pragma unroll
-        for (int h = 0; h < NH; h++)
+            for (int h = 0; h < NH; h++) {
 #pragma unroll
-            for (int p = 0; p < 4; p++)
+                for (int p = 0; p < 4; p++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    // accumulator p carries 2^p (bit p read in place)
-                    sv[h][p][i] = (cs[h][p][i] + dpp_f<0xB1>(cs[h][p][i])) * (1.0f / (float)(1 << p));
+                    for (int i = 0; i < 4; i++) {
+                        const float v0 = (float)ci[h][p][i];
+                        sv[0][p][i] = v0 + 256.0f * dpp_f<0x39>(v0) + 65536.0f * dpp_f<0x4E>(v0);
+                    }
+                if (wr) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        // plus the banked sums of the keys before the last rescale
+                        float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (banked) b = *(const float4*)&bank[64 * h + 4 * (4 * g4 + i)];
+                        const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                        for (int p = 0; p < 4; p++)
+                            accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] =
+                                (sv[0][p][i] + bb[p]) * (1.0f / (float)(1 << p));
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+#pragma unroll
+                for (int p = 0; p < 4; p++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        // accumulator p carries 2^p (bit p read in place)
+                        sv[h][p][i] = (cs[h][p][i] + dpp_f<0xB1>(cs[h][p][i])) * (1.0f / (float)(1 << p));
+        }
         if constexpr (RES) {
 #pragma unroll
             for (int d = 0; d < NB; d++)
@@ -1381,12 +1524,12 @@ void attn_mfma_kernel(AttnArgs a) {
         }
         if (wr) {
 #pragma unroll
-            for (int h = 0; h < NH; h++)
+            for (int h = 0; h < (I8 ? 0 : NH); h++)
 #pragma unroll
                 for (int p = 0; p < 4; p++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = sv[h][p][i];
+                        accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = sv[I8 ? 0 : h][p][i];
             if constexpr (RES) {
 #pragma unroll
                 for (int d = 0; d < NB; d++)
@@ -1405,7 +1548,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 float v = aw[(0 * HP + hs2) * D + e];
                 if (RES) v += aw[(1 * HP + hs2) * D + e];
                 const float f = mfac[w][g];
-                accv += f == 0.0f ? 0.0f : (v * two24 - wofs[w][g]) * f;
+                accv += f == 0.0f ? 0.0f : (v * sunit - wofs[w][g]) * f;
             }
             float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
             dst[2 + e] = accv;
@@ -1491,8 +1634,10 @@ int mfma_wgs_per_cu(int mode, int D, int G) {
 bool mfma_split_ok(int D, int64_t chunk) {
     if (D != 64 && D != 128 && D != 256) return false;
     // buffer offsets are 32-bit and relative to a split's key range; the
-    // prefetches reach up to 12 tiles (768 keys) past its end
-    return (chunk + 1024) * (D / 2) + 4096 < ((int64_t)1 << 31);
+    // prefetches reach up to 12 tiles (768 keys) past its end.  The int8
+    // value path adds at most 2^16 per tile to an int32 accumulator: a wave
+    // takes at most 2^15 tiles (a split below 2^23 keys)
+    return (chunk + 1024) * (D / 2) + 4096 < ((int64_t)1 << 31) && chunk < ((int64_t)1 << 23);
 }
 
 bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {

@@ -115,6 +115,57 @@ def test_many_groups_and_split_phase_api(F, shape):
     close(to_np(outpb).astype(np.float32), refb, what=f"split-phase binary {shape}")
 
 
+def make_rising(B, Hq, Hkv, S, d, seed):
+    """Keys and values that move a wave's running softmax reference and its
+    weight plan mid-stream while the keys before each move still carry a
+    visible share of the output.  Every key sits at score level 0 except,
+    in the second half, one key in 32 at level 1 (about 5.7 above, in log2
+    units) and, in the last quarter, one in 2048 at level 2.  V magnitudes
+    cycle x1, x2, x4, x8 over consecutive 256-key runs, so the tiles that one
+    wave takes (256 keys apart) raise the largest value scale at a power of
+    two up to three times."""
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Hq, d)).astype(np.float16)
+    s = np.arange(S)
+    level = np.zeros(S, np.int64)
+    level[(s >= S // 2) & (s % 32 == 0)] = 1
+    level[(s >= 3 * S // 4) & (s % 2048 == 7)] = 2
+    kmag = np.array([0.1, 0.9, 1.7])[level]
+    # keys agree in sign with their group's first query head on ~75% of dims
+    qh = q.reshape(B, Hkv, Hq // Hkv, d)[:, :, 0].astype(np.float32)
+    agree = rng.random((B, Hkv, S, d)) < 0.75
+    sgn = np.where(agree, np.sign(qh + 1e-30)[:, :, None, :], rng.choice([-1.0, 1.0], size=(B, Hkv, S, d)))
+    k = np.abs(rng.standard_normal((B, Hkv, S, d))) * sgn * kmag[None, None, :, None]
+    vmag = 0.09 * 2.0 ** ((s // 256) % 4)
+    v = rng.standard_normal((B, Hkv, S, d)) * vmag[None, None, :, None]
+    return q, k.astype(np.float16), v.astype(np.float16)
+
+
+@pytest.mark.parametrize("shape", [(2, 16, 16, 8192, 128), (2, 16, 4, 8192, 64), (1, 16, 4, 8192, 256)],
+                         ids=lambda s: str(s))
+def test_rising_scores_and_value_scales(F, shape):
+    """Binary and compensated attention against the oracle on make_rising
+    data: the rescales of a wave's partial sums (a score past the running
+    reference plus its headroom, a value scale past the weight plan) happen
+    mid-stream, between tiles whose keys all contribute."""
+    B, Hq, Hkv, S, d = shape
+    say(f"case rising {shape}")
+    q, k, v = make_rising(B, Hq, Hkv, S, d, seed=11 + d)
+    kb, kr = encode_gpu(F, k)
+    vb, vr = encode_gpu(F, v)
+    qt = torch.from_numpy(q).cuda()
+    kw = dict(n_kv_heads=Hkv) if Hkv != Hq else {}
+    outb = F.binary_attention(qt, kb, vb, B, Hq, S, d, **kw)
+    out = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, **kw)
+    n = B * Hkv * S
+    Kb, Kr = bin_from_blob(kb, n, d), res_from_blob(kr, n, d)
+    Vb, Vr = bin_from_blob(vb, n, d), res_from_blob(vr, n, d)
+    _, refb = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
+    close(to_np(out).astype(np.float32), ref, what=f"compensated {shape}")
+
+
 @pytest.mark.parametrize("H,Hkv,d", [(4, 4, 128), (8, 2, 128), (8, 2, 256)])
 def test_kv_stride_and_zero_length(F, H, Hkv, d):
     say(f"case kv_stride H={H} Hkv={Hkv} d={d}")
