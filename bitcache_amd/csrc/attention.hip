@@ -838,11 +838,14 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
 // The split policy of a full attention call (plan_splits' per_cu): MHA
 // compensated attention several rounds; binary, GQA compensated and adaptive
 // attention one round of what fits of their kernel, at most three workgroups
-// per CU (the adaptive kernel's LDS allows two at d = 128).
+// per CU (the adaptive kernel's LDS allows two at d = 128), binary attention
+// at most two (its tiles are short, so a workgroup's fixed prologue and
+// epilogue weigh more than the latency hiding of a third: c2 54.5 -> 52.9 us).
 int plan_per_cu(int mode, int D, int G) {
     if ((mode == MODE_COMP || mode == MODE_MIXED) && G == 1) return 0;
+    const int cap = mode == MODE_BINARY ? 2 : 3;
     const int n = bc::mfma_wgs_per_cu(mode, D, G);
-    return n <= 0 ? 3 : (n < 3 ? n : 3);
+    return n <= 0 ? cap : (n < cap ? n : cap);
 }
 // the policy of the split-phase entry points (bc_attention_partial and
 // bc_attention_combine, which does not know the mode), and of the fp16

@@ -422,20 +422,20 @@ void attn_mfma_kernel(AttnArgs a) {
     // per CU (measured faster); adaptive mode keeps it
     constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || (MODE == MODE_ADAPTIVE && BC_ADAPT_PIPE) || BC_GQA_PIPE;
     using WL = WaveLds<D, G, RES>;
-    // Binary mode, groups up to 4: the value MFMAs run on int8 operands.  The
-    // sign bits enter in place (element 2^p for bit p of a nibble, four keys
+    // Binary and adaptive modes, groups up to 4: the sign-part value MFMAs
+    // run on int8 operands (the residual part keeps fp16).  The sign bits enter in place (element 2^p for bit p of a nibble, four keys
     // per AND instead of two fp16 elements) and each weight as a 22-bit
     // integer in three balanced 8-bit digit columns (columns 4g + plane, the
     // fourth unused), summed exactly in int32 accumulators that the online
     // softmax rescales by powers of two (integer reference m).
-    constexpr bool I8 = MODE == MODE_BINARY && G <= 4;
+    constexpr bool I8 = (MODE == MODE_BINARY || MODE == MODE_ADAPTIVE) && G <= 4;
     constexpr int kW8Stride = 80;   // bytes per int8 weight column (64 slots + pad)
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
     __shared__ __attribute__((aligned(16))) uint8_t lds_st0[4][WL::kStage];
     __shared__ __attribute__((aligned(16))) uint8_t lds_st1[4][PIPE ? WL::kStage : 16];
-    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][I8 ? 8 : WL::kWeightBytes / 2];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][(I8 && !RES) ? 8 : WL::kWeightBytes / 2];
     __shared__ __attribute__((aligned(16))) int8_t lds_w8[4][I8 ? 4 * G * kW8Stride : 16];
     // (int8 path) per wave and head, the float sums of the keys before the
     // last rescale, [head][D] in the epilogue's dim order
@@ -502,7 +502,10 @@ void attn_mfma_kernel(AttnArgs a) {
 
     // weight column owned by this lane in the MFMA B operand, and its head
     const int my_col = lj;
+    // (int8 path: the sign part's columns are 4 per head, the residual
+    // part's 2 per head as in the fp16 layout)
     const int my_head = I8 ? my_col >> 2 : my_col >> 1;
+    const int my_rhead = my_col >> 1;
     const int bcol = my_col < 2 * G ? my_col : (my_col & 1);
 
     // weight columns [2 parts][2G cols][72 slots]: this lane's store slot in
@@ -1134,6 +1137,7 @@ void attn_mfma_kernel(AttnArgs a) {
 
         // online softmax; (hi, lo) fp16 weights to LDS in MFMA slot order
         float lane_alpha = 1.0f;
+        float lane_ralpha = 1.0f;   // (int8 path) the residual part's head
         bool any_rescale = false;
         // the value operands of odd rows come out 16x larger (see the MFMA
         // loops below): their weights carry 1/16 so that every product is exact
@@ -1144,7 +1148,8 @@ void attn_mfma_kernel(AttnArgs a) {
         // per-key factors shared by the heads: sign weight a2 = p * fa, residual
         // weight b = p * fb, and the offset sum_s (a_s + 8 b_s) grows by p * fo
         const float fa = ldexpf(2.0f * svv * kfac, wexp);
-        const float fb = RES ? ldexpf(rsv * (1.0f / 7.0f) * kfac_res, wexp) : 0.0f;
+        // (int8 path: the fp16 residual weights stay below 2^14 at 2^(wexp - 8))
+        const float fb = RES ? ldexpf(rsv * (1.0f / 7.0f) * kfac_res, wexp - (kWTop - 14)) : 0.0f;
         const float fo_bin = ldexpf(svv, wexp);
         const float fo_res = RES ? ldexpf(svv + rsv * (8.0f / 7.0f), wexp) : fo_bin;
         // residual weights go to the slot of the key's residual position
@@ -1162,6 +1167,7 @@ void attn_mfma_kernel(AttnArgs a) {
                 lsum[g] *= alpha;
                 off[g] *= alpha;
                 if (my_head == g) lane_alpha = alpha;
+                if (I8 && my_rhead == g) lane_ralpha = alpha;
                 any_rescale = true;
                 m[g] = mn;
                 mlim[g] = mn + kTau;
@@ -1217,6 +1223,11 @@ void attn_mfma_kernel(AttnArgs a) {
                 if (my_head >= G) lane_alpha = 1.0f;
                 flush8(lane_alpha * wfac);
             }
+            if (RES && any_rescale) {
+                if (my_rhead >= G) lane_ralpha = 1.0f;
+#pragma unroll
+                for (int d = 0; d < NB; d++) cn[d] *= lane_ralpha;
+            }
         } else if (any_rescale) {
             if (my_head >= G) lane_alpha = 1.0f;
 #pragma unroll
@@ -1247,6 +1258,10 @@ void attn_mfma_kernel(AttnArgs a) {
         v4i_t b8 = v4i_t{0, 0, 0, 0};
         if constexpr (I8) {
             b8 = *(const v4i_t*)w8rd;
+            if constexpr (RES) {
+#pragma unroll
+                for (int mh = 0; mh < 2; mh++) bres[mh] = *(const h8_t*)&wrd[(1 * 2 * G) * WL::kColSlots + 8 * mh];
+            }
         } else {
 #pragma unroll
             for (int mh = 0; mh < 2; mh++) {
@@ -1474,6 +1489,9 @@ void attn_mfma_kernel(AttnArgs a) {
     for (int g0 = 0; g0 < G; g0 += HP) {
         const int hs = my_head - g0;   // this lane's head slot in the batch
         const bool wr = writer && hs >= 0 && hs < HP;
+        // the residual part's writer (fp16 column layout in both paths)
+        const int rhs = my_rhead - g0;
+        const bool rwr = my_col < 2 * G && (my_col & 1) == 0 && rhs >= 0 && rhs < HP;
         if (g0 > 0) __syncthreads();   // the previous batch has been read
         // hi + lo: the neighbour lane's column by DPP (quad_perm [1,0,3,2]),
         // all sums first, then the stores under one branch
@@ -1530,11 +1548,16 @@ void attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         accw[(0 * HP + hs) * D + 64 * h + 4 * (4 * g4 + i) + p] = sv[I8 ? 0 : h][p][i];
-            if constexpr (RES) {
+        }
+        if constexpr (RES) {
+            // (int8 path: the residual part's units of 2^-24, its weights
+            // 2^-8 of the sign weights' scale, become the sign part's units)
+            if (rwr) {
 #pragma unroll
                 for (int d = 0; d < NB; d++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) accw[(1 * HP + hs) * D + 16 * d + 4 * g4 + i] = nv[d][i];
+                    for (int i = 0; i < 4; i++)
+                        accw[(1 * HP + rhs) * D + 16 * d + 4 * g4 + i] = I8 ? nv[d][i] * (two24 * 256.0f) : nv[d][i];
             }
         }
         __syncthreads();

@@ -107,8 +107,8 @@ def test_adaptive_limits(F):
 @pytest.mark.parametrize("S,k", [(10000, 1000), (3000, 300)])
 def test_adaptive_all_keys_tied(F, S, k):
     """Every key of a head equal: one score, so the k keys of lowest index are
-    taken (beyond the sample size the window holds every key and overflows the
-    per-chunk lists: the whole-head select decides)."""
+    taken (the three radix passes end on that score with k ties still to take,
+    and the tie scan places the cutoff index)."""
     say(f"case adaptive all tied S={S}")
     B, Hq, Hkv, d = 1, 4, 2, 128
     q, kx, vx = make(B, Hq, Hkv, S, d, seed=21)

@@ -144,8 +144,8 @@ def make_rising(B, Hq, Hkv, S, d, seed):
 @pytest.mark.parametrize("shape", [(2, 16, 16, 8192, 128), (2, 16, 4, 8192, 64), (1, 16, 4, 8192, 256)],
                          ids=lambda s: str(s))
 def test_rising_scores_and_value_scales(F, shape):
-    """Binary and compensated attention against the oracle on make_rising
-    data: the rescales of a wave's partial sums (a score past the running
+    """Binary, compensated and adaptive (top 10%) attention against the
+    oracle on make_rising data: the rescales of a wave's partial sums (a score past the running
     reference plus its headroom, a value scale past the weight plan) happen
     mid-stream, between tiles whose keys all contribute."""
     B, Hq, Hkv, S, d = shape
@@ -164,6 +164,15 @@ def test_rising_scores_and_value_scales(F, shape):
     _, ref = O.compensated_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
     close(to_np(outb).astype(np.float32), refb, what=f"binary {shape}")
     close(to_np(out).astype(np.float32), ref, what=f"compensated {shape}")
+    top_k = S // 10
+    outa, sel = F.adaptive_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv, top_k=top_k,
+                                     return_selected=True)
+    _, refa, sets = O.adaptive_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, top_k, n_kv_heads=Hkv,
+                                         return_f32=True, return_sets=True)
+    sel = to_np(sel)
+    for (b, h), idx in sets.items():
+        assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"selected set differs at (b={b}, h={h})"
+    close(to_np(outa).astype(np.float32), refa, what=f"adaptive {shape}")
 
 
 @pytest.mark.parametrize("H,Hkv,d", [(4, 4, 128), (8, 2, 128), (8, 2, 256)])
