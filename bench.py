@@ -444,6 +444,17 @@ def main():
         fp16 = {"us_per_step": round(t16 * 1e6, 1), "gbps": round(b16 / t16 / 1e9, 1),
                 "frac_of_peak": round(b16 / t16 / 1e9 / PEAK_HBM_GBS, 4)}
 
+    # the device's streaming-read ceiling (the attention kernels' load policy,
+    # no arithmetic), to read the split kernel's bandwidth against
+    buf = torch.ones(1 << 31, dtype=torch.uint8, device=q.device)
+    _C.read_probe(buf)
+    rd_ms = event_ms(lambda: _C.read_probe(buf), 10, torch)
+    del buf
+    ceiling = (1 << 31) / (rd_ms * 1e-3) / 1e9
+    read_ceiling = {"gbps": round(ceiling, 1), "frac_of_peak": round(ceiling / PEAK_HBM_GBS, 4),
+                    "split_kernel_frac_of_ceiling": round(achieved / ceiling, 4),
+                    "what": "one nontemporal 16-byte-load read of 2 GiB (bc_read_probe)"}
+
     traffic = traffic_from_profiles()
     out = {
         "metric": METRIC,
@@ -467,6 +478,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic, "kernel": "attn_mfma_kernel<128,1,COMP>",
                      "kernel_us": round(split_ms * 1e3, 1)},
+        "read_ceiling": read_ceiling,
         "fp16_reference": fp16,
         "speedup_vs_fp16": (round(fp16["us_per_step"] / (wall * 1e6), 3) if fp16 else None),
     }

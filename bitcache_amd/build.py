@@ -28,7 +28,7 @@ EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 EXT = os.path.join(HERE, "_C" + EXT_SUFFIX)
 
 HIP_SOURCES = ["encode.hip", "attention.hip", "attention_mfma.hip", "adaptive.hip", "convert.hip",
-               "abi.cpp"]
+               "probe.hip", "abi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -163,6 +163,19 @@ void encode_traffic_probe(torch::Tensor src, torch::Tensor bin, torch::Tensor re
                  "encode_traffic_probe");
 }
 
+// The device's streaming-read ceiling: reads src's bytes once (measurement
+// aid); returns the output words, of which the first 4 per workgroup (four
+// workgroups per CU, at most one per 16 bytes) hold the per-wave XORs
+torch::Tensor read_probe(torch::Tensor src) {
+    TORCH_CHECK(src.is_cuda() && src.is_contiguous(), "src must be a contiguous device tensor");
+    const int64_t n = src.numel() * src.element_size();
+    TORCH_CHECK(n % 16 == 0, "src must hold a multiple of 16 bytes");
+    c10::DeviceGuard guard(src.device());
+    auto out = torch::empty({BC_READ_PROBE_OUT_WORDS}, src.options().dtype(torch::kInt32));
+    check_status(bc_read_probe(src.data_ptr(), n, out.data_ptr(), stream_of(src)), "read_probe");
+    return out;
+}
+
 void check_kv_token(const torch::Tensor& kv, int64_t batch, int64_t n_heads, int64_t d) {
     BC_CHECK_INPUT(kv);
     TORCH_CHECK(kv.numel() == batch * n_heads * d, "kv must hold batch*n_heads*head_dim values");
@@ -601,6 +614,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("fp32_scale") = false);
     m.def("encode_traffic_probe", &encode_traffic_probe,
           "encode_fused's loads and stores without its arithmetic (memory floor)");
+    m.def("read_probe", &read_probe, "One streaming read of a tensor's bytes (the read ceiling)");
     m.def("online_encode_kv", &online_encode_kv, "K and V token encode in one launch");
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
     m.def("encode_into_cache_bshd", &encode_into_cache_bshd,

@@ -122,6 +122,17 @@ int bc_online_encode_kv(const void* k, const void* v, void* k_bin, void* k_res, 
 int bc_encode_traffic_probe(const void* src, void* binary_blob, void* residual_blob,
                             int64_t n_vecs, int head_dim, void* stream);
 
+/* The device's streaming-read ceiling: reads n_bytes (a multiple of 16, src
+ * 16-byte aligned) once with the nontemporal 16-byte loads the attention
+ * kernels use for whole-KiB runs, spread over four workgroups per CU, and
+ * writes one XOR word per wave into out (room for BC_READ_PROBE_OUT_WORDS
+ * uint32).  Time it to read the attention kernels' bandwidth against what
+ * the memory system delivers.  No counterpart in the reference; a
+ * measurement aid for benchmarks. */
+#define BC_READ_PROBE_MAX_WGS 4096
+#define BC_READ_PROBE_OUT_WORDS (4 * BC_READ_PROBE_MAX_WGS)
+int bc_read_probe(const void* src, int64_t n_bytes, void* out, void* stream);
+
 /* ---- attention -------------------------------------------------------------- */
 /* Bytes of scratch the attention entry points need for this shape on the
  * current device (split-KV partial results).  Callers allocate it; it may be

@@ -93,6 +93,13 @@ def test_encode_argument_errors(lib, no_gpu):
     assert t(fake, fake, fake, -1, 128, None) == BC_ERR_INVALID_ARGUMENT
     assert t(fake, None, fake, 10, 128, None) == BC_ERR_INVALID_ARGUMENT
     assert t(None, None, None, 0, 128, None) == BC_OK
+    r = lib.bc_read_probe
+    r.argtypes = [P, ctypes.c_int64, P, P]
+    assert r(fake, 24, fake, None) == BC_ERR_INVALID_ARGUMENT        # not a multiple of 16
+    assert r(fake, -16, fake, None) == BC_ERR_INVALID_ARGUMENT
+    assert r(None, 64, fake, None) == BC_ERR_INVALID_ARGUMENT
+    assert r(P(0x1008), 64, fake, None) == BC_ERR_INVALID_ARGUMENT   # unaligned
+    assert r(None, 0, None, None) == BC_OK
 
 
 def test_attention_argument_errors(lib, no_gpu):

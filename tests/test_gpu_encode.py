@@ -261,6 +261,25 @@ def test_encode_prefill_scale_property(F):
     assert np.array_equal(gr.codes[idx], er.codes)
 
 
+@pytest.mark.parametrize("n_bytes", [16, 4096 * 16 + 48, 3 << 20])
+def test_read_probe_reads_every_word_once(n_bytes):
+    """The read-ceiling probe's per-wave XOR words combine to the XOR of every
+    32-bit word of the source: each 16-byte piece is read (an odd number of
+    times, i.e. once), the ragged tail and a source smaller than the grid
+    included."""
+    from bitcache_amd import _C
+    say(f"case read probe {n_bytes}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(n_bytes)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n_bytes // 4,), dtype=torch.int32, device="cuda", generator=g)
+    out = _C.read_probe(src)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wgs = min(cus * 4, 4096, n_bytes // 16)
+    got = np.bitwise_xor.reduce(out[: 4 * wgs].cpu().numpy())
+    want = np.bitwise_xor.reduce(src.cpu().numpy())
+    assert got == want
+
+
 @pytest.mark.parametrize("d,n", [(64, 5000), (128, 3001), (256, 777)])
 def test_traffic_probe_stays_in_its_blobs(d, n):
     """The encoder's traffic probe (same loads and stores, no arithmetic)
