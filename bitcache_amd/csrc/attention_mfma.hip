@@ -178,14 +178,25 @@ __device__ __forceinline__ int mbcnt64(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Workgroup barrier for data exchanged through LDS only: this wave's LDS
+// stores have completed (lgkmcnt), the compiler moves no memory access across
+// it, and loads in flight (the first tile's, some into other LDS arrays) stay
+// in flight.  A __syncthreads() would also wait for every direct-to-LDS load.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Query preparation of one workgroup (256 threads), spread over all threads:
 // the query as floats and its sign words (a wave ballot per 64 elements);
 // scale_q (sequential fp32 order, element 0 first) and the fixed-point step
 // per head; q_int = rint(q / step) per element (in place of the floats); then
 // the balanced int4 digit words (one (word, digit) pair per thread) and the
 // int8 MFMA operand words.
-template <int D, int G, bool KMF>
-__device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf) {
+template <int D, int G, bool KMF, int NQ>
+__device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float* qf) {
     static_assert((G * D) % 64 == 0, "whole waves of query elements");
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t* signs = &qd.signs[0][0];   // [G * D / 32] words, bit b of word i = element 32i + b
@@ -193,9 +204,12 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
     // the three int8 planes of q_int per element (int8 MFMA operands)
     __shared__ __attribute__((aligned(8))) uint8_t pbytes[KMF ? 3 : 1][KMF ? G * D : 8];
     // floats, sign words (wave ballots) and each wave's max |q| (its 64
-    // elements lie in one head)
-    for (int i = tid; i < G * D; i += 256) {
-        const float x = h2f(qbase[i]);
+    // elements lie in one head); element tid + 256j was loaded into qpre[j]
+#pragma unroll
+    for (int j = 0; j < NQ; j++) {
+        const int i = tid + 256 * j;
+        if (i >= G * D) break;   // (whole waves)
+        const float x = h2f(qpre[j]);
         qf[i] = x;
         const uint64_t bits = __ballot(x >= 0.0f);
         const float wm = wave_max(fabsf(x));
@@ -205,7 +219,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
             gmax[i / 64] = wm;
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < G) {
         // sequential fp32 order (element 0 first), eight float4 reads in
         // flight at a time
@@ -227,7 +241,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
         for (int k = 0; k < D / 64; k++) mx = fmaxf(mx, gmax[tid * (D / 64) + k]);
         qd.dq[tid] = mx > 0.0f ? 256.0f * (mx / kQIntMax) : 256.0f;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) {
         float m = 0.0f;
         for (int g = 0; g < G; g++) m = fmaxf(m, qd.dq[g]);
@@ -248,7 +262,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
             pbytes[2][i] = (uint8_t)((t1 - p1) >> 8);
         }
     }
-    __syncthreads();
+    lds_barrier();
     // digit j of the 8 elements of word w: nibble k = element 8w + k (balanced
     // base 16: t = sum_j d_j 16^j, d_j in [-8, 7]).  Four threads per word
     // (a DPP quad), two elements each; the quad ORs its nibbles together.
@@ -318,7 +332,7 @@ __device__ void prep_digits(const uint16_t* qbase, QDigits<D, G>& qd, float* qf)
             if constexpr (!LO_COLS) qd.bq_lo[pc][h][ln] = make_int4(wl[0], wl[1], wl[2], wl[3]);
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Build-time switches; each default is the measured fastest on MI355X:
@@ -453,8 +467,6 @@ void attn_mfma_kernel(AttnArgs a) {
     const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
     const int bhq0 = b * a.Hq + hq0;
 
-    prep_digits<D, G, KMF>(a.q + (int64_t)bhq0 * D, qd, qf);
-
     // the wave index is uniform: readfirstlane lets the compiler keep the tile
     // loop in scalar registers (a uniform loop, not an exec-masked one)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -472,6 +484,148 @@ void attn_mfma_kernel(AttnArgs a) {
     // the copy permutes the pieces within each row (same cache lines).  A
     // lane's transposed reads cover row = lane.
     const int vsw = ((lane * CB) >> 8) & (Q - 1);
+
+    // Buffer resources over this workgroup's key range [key_begin, key_end)
+    // of each plane: offsets are 32-bit and tile-relative, and a load of a key
+    // past the range returns zeros (its weight is 0), so no lane clamps its
+    // address and every lane issues the same loads (the wait counts stay exact)
+    const int nk = max(key_end - key_begin, 0);   // (an empty split issues no loads)
+    auto rsrc = [&](const void* plane, int rb) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const uint8_t*)plane + (kv_base + key_begin) * rb), (short)0, nk * rb, kBufWord3);
+    };
+    const __amdgpu_buffer_rsrc_t r_ks = rsrc(a.kb.signs, SB), r_vs = rsrc(a.vb.signs, SB);
+    const __amdgpu_buffer_rsrc_t r_ksc = rsrc(a.kb.scales, 2), r_vsc = rsrc(a.vb.scales, 2);
+    const __amdgpu_buffer_rsrc_t r_kc = rsrc(a.kr.codes, CB), r_vc = rsrc(a.vr.codes, CB);
+    const __amdgpu_buffer_rsrc_t r_krs = rsrc(a.kr.scales, 2), r_vrs = rsrc(a.vr.scales, 2);
+    // adaptive: stored popcounts of this group, one pack of G per key
+    using Pack = bc::PcPack<bc::PcT<D>, G>;
+    constexpr int kPack = (int)sizeof(Pack);
+    static_assert(kPack <= 16, "one load per pack");
+    const __amdgpu_buffer_rsrc_t r_pc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S) + key_begin), (short)0, nk * kPack, kBufWord3);
+    // an offset past every range (the host keeps each range's bytes below
+    // 2^31 - 4096): such a load returns zeros and moves no data
+    constexpr int kOob = 0x7FFFF000;
+
+    // ---------------- loads of one tile: K side into registers, V side to LDS
+    auto load_k = [&](KRegs<D>& r, int t0) {
+        const int tr = t0 - key_begin;      // tile offset in the range (keys)
+        const int kk = tr + kown;
+        if constexpr (MODE == MODE_ADAPTIVE) {
+            // popcounts and the two binary scales; residual data is gathered
+            // once the tile's selection is known
+            if constexpr (kPack == 1) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b8(r_pc, kk, 0, 0);
+            } else if constexpr (kPack == 2) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b16(r_pc, kk * 2, 0, 0);
+            } else if constexpr (kPack == 4) {
+                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b32(r_pc, kk * 4, 0, 0);
+            } else if constexpr (kPack == 8) {
+                const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r_pc, kk * 8, 0, 0);
+                r.pcw[0] = v[0]; r.pcw[1] = v[1];
+            } else {
+                const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pc, kk * 16, 0, 0);
+                r.pcw[0] = v[0]; r.pcw[1] = v[1]; r.pcw[2] = v[2]; r.pcw[3] = v[3];
+            }
+            r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
+            r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
+            r.rsk = 0;
+            r.rsv = 0;
+            return;
+        }
+        r.ks = buf_signs<D, BC_NT_AUX>(r_ks, kk * SB);
+        r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, BC_NT_SCALES);
+        r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, BC_NT_SCALES);
+        r.rsk = 0;
+        r.rsv = 0;
+        // residual scales and K codes of every key (adaptive mode too: the
+        // selection is known only after the scores, and these loads are the
+        // ones worth prefetching; V codes are gathered for selected keys)
+        if constexpr (RES) {
+            r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, kk * 2, 0, BC_NT_SCALES);
+            r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, kk * 2, 0, BC_NT_SCALES);
+            if constexpr (KMF) {
+                // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
+                const int base = (tr + (lane & 15)) * CB + 16 * (lane >> 4);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int pc = 0; pc < NPC; pc++) {
+                        const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 16 * kb * CB + 64 * pc, 0, BC_NT_AUX);
+                        const int i = kb * NPC + pc;
+                        r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
+                    }
+            } else {
+                // per key: the lane's own row; linear: piece i*1024 + 16l of the tile
+                const int base = LIN_K ? tr * CB + 16 * lane : kk * CB;
+#pragma unroll
+                for (int i = 0; i < Q; i++) {
+                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + (LIN_K ? i * 1024 : 16 * i), 0,
+                                                                          LIN_K ? BC_NT_AUX : 0);
+                    r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
+                }
+            }
+        }
+    };
+    // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear,
+    // pieces swizzled as above) or piece c at c*1024 + 16k (per key)
+    auto issue_v = [&](int buf, int t0) {
+        const int tr = t0 - key_begin;
+        uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
+        uint8_t* st_signs = st_codes + WL::kCodeBytes;
+        if constexpr (SB >= 16) {
+#pragma unroll
+            for (int c = 0; c < SB / 16; c++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs + c * 1024), 16,
+                                                         tr * SB + 16 * lane + c * 1024, 0, 0, BC_NT_AUX);
+        } else {
+            // 8-byte rows: one KiB load covers 128 rows, so lanes 32..63 repeat
+            // lanes 0..31 (into bytes 512..1023)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs), 16,
+                                                     tr * SB + 16 * (lane & 31), 0, 0, 0);
+        }
+        if constexpr (ALLRES) {
+#pragma unroll
+            for (int c = 0; c < Q; c++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
+                    LIN_V ? tr * CB + c * 1024 + 16 * (lane ^ ((4 * c + (lane >> 4)) & (Q - 1)))
+                          : (tr + lane) * CB + 16 * c, 0, 0, LIN_V ? BC_NT_AUX : 0);
+        }
+    };
+
+    // The query's elements are loaded first, then the wave's first tile
+    // (except in adaptive mode, whose first tile needs the selection, and in
+    // the workgroup that appends a token), and the query preparation runs
+    // while that tile is in flight: it waits only for the older query loads,
+    // and its barriers wait for LDS traffic only.
+    constexpr int NQ = (G * D + 255) / 256;
+    uint16_t qpre[NQ];
+    {
+        const uint16_t* qb = a.q + (int64_t)bhq0 * D;
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            const int i = (int)threadIdx.x + 256 * j;
+            qpre[j] = i < G * D ? qb[i] : (uint16_t)0;
+        }
+    }
+    const bool app_here = a.app_k != nullptr && a.app_slot >= key_begin && a.app_slot < key_end;
+    int t = key_begin + wave * 64;
+    const bool early = MODE != MODE_ADAPTIVE && !app_here && t < key_end;
+    KRegs<D> ka, kb;
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MODE != MODE_ADAPTIVE) {
+        // without a first tile to fetch, the same loads address keys past the
+        // range (a split holds fewer than 2^23 keys): zeros, no traffic, and
+        // the same instructions on every path, so that the preparation's
+        // wait for the query counts them exactly
+        const int t_first = early ? t : key_begin + (1 << 23) + 1024;
+        load_k(ka, t_first);
+        issue_v(0, t_first);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    prep_digits<D, G, KMF>(qpre, qd, qf);
 
     // In-place append: the workgroup whose key range holds the new token's slot
     // encodes the token's K and V vectors into the cache first (wave 0, lane
@@ -634,116 +788,6 @@ void attn_mfma_kernel(AttnArgs a) {
                 bq[pc][h] = v4i_t{w.x, w.y, w.z, w.w};
             }
     }
-
-    // Buffer resources over this workgroup's key range [key_begin, key_end)
-    // of each plane: offsets are 32-bit and tile-relative, and a load of a key
-    // past the range returns zeros (its weight is 0), so no lane clamps its
-    // address and every lane issues the same loads (the wait counts stay exact)
-    const int nk = max(key_end - key_begin, 0);   // (an empty split issues no loads)
-    auto rsrc = [&](const void* plane, int rb) {
-        return __builtin_amdgcn_make_buffer_rsrc(
-            (void*)((const uint8_t*)plane + (kv_base + key_begin) * rb), (short)0, nk * rb, kBufWord3);
-    };
-    const __amdgpu_buffer_rsrc_t r_ks = rsrc(a.kb.signs, SB), r_vs = rsrc(a.vb.signs, SB);
-    const __amdgpu_buffer_rsrc_t r_ksc = rsrc(a.kb.scales, 2), r_vsc = rsrc(a.vb.scales, 2);
-    const __amdgpu_buffer_rsrc_t r_kc = rsrc(a.kr.codes, CB), r_vc = rsrc(a.vr.codes, CB);
-    const __amdgpu_buffer_rsrc_t r_krs = rsrc(a.kr.scales, 2), r_vrs = rsrc(a.vr.scales, 2);
-    // adaptive: stored popcounts of this group, one pack of G per key
-    using Pack = bc::PcPack<bc::PcT<D>, G>;
-    constexpr int kPack = (int)sizeof(Pack);
-    static_assert(kPack <= 16, "one load per pack");
-    const __amdgpu_buffer_rsrc_t r_pc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S) + key_begin), (short)0, nk * kPack, kBufWord3);
-    // an offset past every range (the host keeps each range's bytes below
-    // 2^31 - 4096): such a load returns zeros and moves no data
-    constexpr int kOob = 0x7FFFF000;
-
-    // ---------------- loads of one tile: K side into registers, V side to LDS
-    auto load_k = [&](KRegs<D>& r, int t0) {
-        const int tr = t0 - key_begin;      // tile offset in the range (keys)
-        const int kk = tr + kown;
-        if constexpr (MODE == MODE_ADAPTIVE) {
-            // popcounts and the two binary scales; residual data is gathered
-            // once the tile's selection is known
-            if constexpr (kPack == 1) {
-                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b8(r_pc, kk, 0, 0);
-            } else if constexpr (kPack == 2) {
-                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b16(r_pc, kk * 2, 0, 0);
-            } else if constexpr (kPack == 4) {
-                r.pcw[0] = __builtin_amdgcn_raw_buffer_load_b32(r_pc, kk * 4, 0, 0);
-            } else if constexpr (kPack == 8) {
-                const v2u_t v = __builtin_amdgcn_raw_buffer_load_b64(r_pc, kk * 8, 0, 0);
-                r.pcw[0] = v[0]; r.pcw[1] = v[1];
-            } else {
-                const v4u_t v = __builtin_amdgcn_raw_buffer_load_b128(r_pc, kk * 16, 0, 0);
-                r.pcw[0] = v[0]; r.pcw[1] = v[1]; r.pcw[2] = v[2]; r.pcw[3] = v[3];
-            }
-            r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, 0);
-            r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, 0);
-            r.rsk = 0;
-            r.rsv = 0;
-            return;
-        }
-        r.ks = buf_signs<D, BC_NT_AUX>(r_ks, kk * SB);
-        r.sk = __builtin_amdgcn_raw_buffer_load_b16(r_ksc, kk * 2, 0, BC_NT_SCALES);
-        r.svv = __builtin_amdgcn_raw_buffer_load_b16(r_vsc, kk * 2, 0, BC_NT_SCALES);
-        r.rsk = 0;
-        r.rsv = 0;
-        // residual scales and K codes of every key (adaptive mode too: the
-        // selection is known only after the scores, and these loads are the
-        // ones worth prefetching; V codes are gathered for selected keys)
-        if constexpr (RES) {
-            r.rsk = __builtin_amdgcn_raw_buffer_load_b16(r_krs, kk * 2, 0, BC_NT_SCALES);
-            r.rsv = __builtin_amdgcn_raw_buffer_load_b16(r_vrs, kk * 2, 0, BC_NT_SCALES);
-            if constexpr (KMF) {
-                // key block kb: key 16kb + l%16, 16-byte piece l/16 + 4pc of its row
-                const int base = (tr + (lane & 15)) * CB + 16 * (lane >> 4);
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int pc = 0; pc < NPC; pc++) {
-                        const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + 16 * kb * CB + 64 * pc, 0, BC_NT_AUX);
-                        const int i = kb * NPC + pc;
-                        r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
-                    }
-            } else {
-                // per key: the lane's own row; linear: piece i*1024 + 16l of the tile
-                const int base = LIN_K ? tr * CB + 16 * lane : kk * CB;
-#pragma unroll
-                for (int i = 0; i < Q; i++) {
-                    const v4u_t c = __builtin_amdgcn_raw_buffer_load_b128(r_kc, base + (LIN_K ? i * 1024 : 16 * i), 0,
-                                                                          LIN_K ? BC_NT_AUX : 0);
-                    r.kc[4 * i] = c[0]; r.kc[4 * i + 1] = c[1]; r.kc[4 * i + 2] = c[2]; r.kc[4 * i + 3] = c[3];
-                }
-            }
-        }
-    };
-    // V tile to LDS: key k's sign row at k*SB; its code row at k*CB (linear,
-    // pieces swizzled as above) or piece c at c*1024 + 16k (per key)
-    auto issue_v = [&](int buf, int t0) {
-        const int tr = t0 - key_begin;
-        uint8_t* st_codes = buf ? lds_st1[wave] : lds_st0[wave];
-        uint8_t* st_signs = st_codes + WL::kCodeBytes;
-        if constexpr (SB >= 16) {
-#pragma unroll
-            for (int c = 0; c < SB / 16; c++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs + c * 1024), 16,
-                                                         tr * SB + 16 * lane + c * 1024, 0, 0, BC_NT_AUX);
-        } else {
-            // 8-byte rows: one KiB load covers 128 rows, so lanes 32..63 repeat
-            // lanes 0..31 (into bytes 512..1023)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_vs, LDS_PTR(void, st_signs), 16,
-                                                     tr * SB + 16 * (lane & 31), 0, 0, 0);
-        }
-        if constexpr (ALLRES) {
-#pragma unroll
-            for (int c = 0; c < Q; c++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    r_vc, LDS_PTR(void, st_codes + c * 1024), 16,
-                    LIN_V ? tr * CB + c * 1024 + 16 * (lane ^ ((4 * c + (lane >> 4)) & (Q - 1)))
-                          : (tr + lane) * CB + 16 * c, 0, 0, LIN_V ? BC_NT_AUX : 0);
-        }
-    };
 
     // ---------------- adaptive mode: a tile's selection, from its stored
     // popcounts and K scales, and the loads of its residual data: the residual
@@ -1374,8 +1418,6 @@ void attn_mfma_kernel(AttnArgs a) {
     // LDS per staging buffer only within an iteration (across the back edge it
     // would wait for all of them at the first staging-buffer read), so the
     // prefetch issued before an iteration's second tile lands by its end.
-    int t = key_begin + wave * 64;
-
     if constexpr (MODE == MODE_ADAPTIVE) {
         // popcounts and binary scales two tiles ahead, selection and residual
         // gathers one tile ahead; each iteration (two tiles) starts with no
@@ -1411,18 +1453,22 @@ void attn_mfma_kernel(AttnArgs a) {
             __builtin_amdgcn_wave_barrier();
         }
     } else if (!PIPE) {
+        bool issued = early;   // (the first tile's loads went out before the preparation)
         for (; t < key_end; t += 4 * 64) {
-            KRegs<D> ka;
-            load_k(ka, t);
-            issue_v(0, t);
+            if (!issued) {
+                load_k(ka, t);
+                issue_v(0, t);
+            }
+            issued = false;
             process(ka, t, 0);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
     } else if (t < key_end) {
-        KRegs<D> ka, kb;
-        load_k(ka, t);
-        issue_v(0, t);
+        if (!early) {
+            load_k(ka, t);
+            issue_v(0, t);
+        }
         __builtin_amdgcn_s_waitcnt(0);
         for (;;) {
             int tp = t + 4 * 64;
