@@ -5,21 +5,27 @@
 // group), 4 wave64 per workgroup, 64-key tiles round-robin over the waves.
 //
 // Score phase (lane = key): XNOR popcount of the sign words, and the INT4
-// residual dot with v_dot8_i32_i4 directly on the stored two's-complement
-// nibbles against the query quantised to 16-bit fixed point and split into
-// four balanced int4 digits (q_int = d0 + 16 d1 + 256 d2 + 4096 d3).
+// residual dot directly on the stored two's-complement nibbles against the
+// query in 24-bit fixed point: six balanced int4 digits for v_dot8_i32_i4
+// (MHA) or three balanced int8 planes for an int8 MFMA (GQA groups), of which
+// a tile uses the top 16 bits unless a key's residual scale makes it a
+// precise tile.
 //
 // Value phase: out[e] = sum_s a_s*(2*bit_se - 1) + b_s*(u_se - 8) with
 // a = p*sv, b = p*rs/7, u = n + 8.  The V tile (sign bytes and code bytes of
 // 64 keys) is copied to LDS with direct buffer loads, then ds_read_b64_tr_b4
 // transposes 16 keys x 16 nibbles per 16-lane group so that each lane holds
-// 16 keys of one dimension.  Nibbles (u) and sign bits become exact fp16
-// subnormals (value * 2^(j-24) for bit position j < 10) with one mask per
-// pair of keys, left in place (the power of two is folded into the weights
-// of odd keys and into the accumulator of bit p), and
+// 16 keys of one dimension.  fp16 path: nibbles (u) and sign bits become
+// exact fp16 subnormals (value * 2^(j-24) for bit position j < 10) with one
+// mask per pair of keys, left in place (the power of two is folded into the
+// weights of odd keys and into the accumulator of bit p), and
 // v_mfma_f32_16x16x32_f16 accumulates dims x weight-columns, where the weight
 // columns are (hi, lo) fp16 splits of a and b for each query head of the
-// group.  The fp32 accumulators are rescaled on running-max changes.
+// group; the fp32 accumulators are rescaled on running-max changes.  int8
+// path (the sign part of binary and adaptive attention, groups up to 4):
+// sign bits in place as int8 elements, four keys per mask, weights as
+// balanced 8-bit digit columns, exact int32 sums flushed into a float bank on
+// rescales (see I8 below).
 #include <math.h>
 
 #include "attn.h"
@@ -437,11 +443,13 @@ void attn_mfma_kernel(AttnArgs a) {
     constexpr bool PIPE = (G == 1 && BC_MHA_PIPE) || (MODE == MODE_ADAPTIVE && BC_ADAPT_PIPE) || BC_GQA_PIPE;
     using WL = WaveLds<D, G, RES>;
     // Binary and adaptive modes, groups up to 4: the sign-part value MFMAs
-    // run on int8 operands (the residual part keeps fp16).  The sign bits enter in place (element 2^p for bit p of a nibble, four keys
-    // per AND instead of two fp16 elements) and each weight as a 22-bit
-    // integer in three balanced 8-bit digit columns (columns 4g + plane, the
-    // fourth unused), summed exactly in int32 accumulators that the online
-    // softmax rescales by powers of two (integer reference m).
+    // run on int8 operands (the residual part keeps fp16).  The sign bits
+    // enter in place (element 2^p for bit p of a nibble, four keys per AND
+    // instead of two fp16 elements) and each weight as an integer below 2^22
+    // in three balanced 8-bit digit columns (columns 4g + plane, the fourth
+    // unused), summed exactly in int32 accumulators.  A rescale (running max
+    // or weight plan) flushes those sums, scaled, into a per-wave float bank
+    // in LDS and restarts them at zero (flush8).
     constexpr bool I8 = (MODE == MODE_BINARY || MODE == MODE_ADAPTIVE) && G <= 4;
     constexpr int kW8Stride = 80;   // bytes per int8 weight column (64 slots + pad)
 
