@@ -933,7 +933,9 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
                 int kv_stride, int head_dim, void* workspace, size_t workspace_bytes,
                 hipStream_t st, const uint32_t* thresh, const int32_t* cutoff,
                 uint8_t* selected, const void* pcs, int per_cu, const AppendArgs* app = nullptr,
-                const uint8_t* head_mode = nullptr) {
+                const uint8_t* head_mode = nullptr, void* direct_out = nullptr,
+                bool* wrote_out = nullptr) {
+    if (wrote_out) *wrote_out = false;
     int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
     if (v != BC_OK) return v;
     if ((int64_t)batch * n_heads == 0) return BC_OK;
@@ -971,9 +973,15 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     }
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     // matrix-core value phase for head_dim 64/128/256; the VALU kernel covers the
-    // other head dims (and is selectable with BITCACHE_VALU_ATTENTION=1)
-    if (!valu_forced() && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st))
+    // other head dims (and is selectable with BITCACHE_VALU_ATTENTION=1).  With
+    // one split per group the matrix-core kernel normalises and writes the
+    // output itself (no merge launch).
+    if (direct_out != nullptr && p.n_splits == 1) a.out = (uint16_t*)direct_out;
+    if (!valu_forced() && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st)) {
+        if (wrote_out) *wrote_out = a.out != nullptr;
         return bc::check_launch("attention split (mfma)");
+    }
+    a.out = nullptr;
     // (the VALU kernel does not append; the append entry point checks first)
     BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
     BC_REQUIRE(mode != MODE_MIXED, BC_ERR_UNSUPPORTED,
@@ -1002,12 +1010,13 @@ int run_attention(int mode, const void* q, const void* k_bin, const void* k_res,
                   const uint8_t* head_mode) {
     const int per_cu = head_dim > 0 && n_kv_heads > 0
                            ? plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads)) : kPlanFixed;
-    int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
-                         kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
-                         selected, pcs, per_cu, app, head_mode);
-    if (rc != BC_OK) return rc;
     BC_REQUIRE(out != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null output");
+    bool wrote = false;
+    int rc = run_partial(mode, q, k_bin, k_res, v_bin, v_res, batch, n_heads, n_kv_heads, seq_len,
+                         kv_stride, head_dim, workspace, workspace_bytes, st, thresh, cutoff,
+                         selected, pcs, per_cu, app, head_mode, out, &wrote);
+    if (rc != BC_OK || wrote) return rc;
     return run_combine(per_cu, workspace, out, batch, n_heads, n_kv_heads, seq_len, head_dim, st);
 }
 

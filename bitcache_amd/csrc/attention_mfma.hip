@@ -1627,11 +1627,18 @@ void attn_mfma_kernel(AttnArgs a) {
                 const float f = mfac[w][g];
                 accv += f == 0.0f ? 0.0f : (v * sunit - wofs[w][g]) * f;
             }
-            float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
-            dst[2 + e] = accv;
-            if (e == 0) {
-                dst[0] = hsum[0][g];
-                dst[1] = hsum[1][g];
+            if (a.out != nullptr) {
+                // one split: the output itself, normalised as the merge of a
+                // single partial would (factor 1, sum l)
+                const float L = hsum[1][g];
+                a.out[(int64_t)(bhq0 + g) * D + e] = f2h(L > 0.0f ? accv * (1.0f / L) : 0.0f);
+            } else {
+                float* dst = a.ws + ((int64_t)(bhq0 + g) * a.n_splits + split) * (D + 2);
+                dst[2 + e] = accv;
+                if (e == 0) {
+                    dst[0] = hsum[0][g];
+                    dst[1] = hsum[1][g];
+                }
             }
         }
     }

@@ -37,6 +37,10 @@ struct AttnArgs {
     int app_slot;
     // MODE_MIXED: [B*Hq] 0 = binary attention for that head, else compensated
     const uint8_t* head_mode;
+    // one split per group (n_splits == 1): when set, the kernel writes the
+    // normalised output [B, Hq, D] fp16 here instead of its partial, and no
+    // merge launch follows
+    uint16_t* out;
 };
 
 // Packs per row of the stored popcounts: S rounded up to 16, so that every
