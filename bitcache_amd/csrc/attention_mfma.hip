@@ -200,8 +200,8 @@ __device__ __forceinline__ void lds_barrier() {
 // scale_q (sequential fp32 order, element 0 first) and the fixed-point step
 // per head; q_int = rint(q / step) per element (in place of the floats); then
 // the balanced int4 digit words (one (word, digit) pair per thread) and the
-// int8 MFMA operand words.
-template <int D, int G, bool KMF, int NQ>
+// int8 MFMA operand words (the fixed-point parts only for residual modes).
+template <int D, int G, bool KMF, bool RES, int NQ>
 __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float* qf) {
     static_assert((G * D) % 64 == 0, "whole waves of query elements");
     const int tid = threadIdx.x, lane = tid & 63;
@@ -248,6 +248,8 @@ __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float
         qd.dq[tid] = mx > 0.0f ? 256.0f * (mx / kQIntMax) : 256.0f;
     }
     lds_barrier();
+    // binary attention needs only the sign words and scale_q
+    if constexpr (!RES) return;
     if (tid == 0) {
         float m = 0.0f;
         for (int g = 0; g < G; g++) m = fmaxf(m, qd.dq[g]);
@@ -633,7 +635,7 @@ void attn_mfma_kernel(AttnArgs a) {
         issue_v(0, t_first);
     }
     __builtin_amdgcn_sched_barrier(0);
-    prep_digits<D, G, KMF>(qpre, qd, qf);
+    prep_digits<D, G, KMF, RES>(qpre, qd, qf);
 
     // In-place append: the workgroup whose key range holds the new token's slot
     // encodes the token's K and V vectors into the cache first (wave 0, lane
