@@ -47,6 +47,8 @@ SHAPES = [
     (1, 8, 1, 513, 128),      # GQA 8
     (1, 6, 2, 300, 128),      # GQA 3 (query heads processed one by one)
     (1, 4, 2, 700, 128),      # GQA 2 (int8-MFMA residual dots)
+    (2, 4, 2, 333, 64),       # GQA 2 at d = 64 (binary: int8 value path, two heads)
+    (1, 4, 2, 301, 256),      # GQA 2 at d = 256
     (2, 8, 2, 333, 64),       # GQA 4 at d = 64 (lane-piece residual dots)
     (1, 8, 2, 500, 256),      # GQA 4 at d = 256 (two code pieces per lane)
     (1, 16, 2, 300, 256),     # GQA 8 at d = 256
