@@ -1,27 +1,40 @@
 // Adaptive precision: exact top-k residual selection per (b, query head).
 //
 // The ranking key of key s is scale_k * (2*popcount - d) (exact in fp32),
-// mapped to an order-preserving uint32 u.  The k-th largest u is found by a
-// radix select over three digits (bits 31..21, 20..10, 9..0): each pass
-// histograms the digit of the keys that still match the prefix found so far
-// (one LDS histogram per key chunk, stored whole), and a one-block scan per
-// (b, head) sums the chunks and picks the digit where the running count from
-// the top reaches k.  After the third pass the threshold T and the number
-// `need` of keys equal to T that are still to be taken are exact.  Ties at T
-// are taken in key order, i.e. up to a cutoff key index: the third pass's
-// chunk histograms locate the chunk holding the need-th tie; one block per
-// (b, head) then scans only that chunk for the cutoff index.  The attention
-// kernel selects key > T, or key == T at an index <= cutoff.  Passes, tie
-// scan and attention compare exact float scores against bounds derived from
-// the key prefix (see key_floor), which order like the keys.
+// mapped to an order-preserving uint32 (ordered_key).  The k-th largest key T
+// and the tie cutoff come from four launches:
+//   1. hist_kernel: the popcounts of every key from the K sign planes, stored
+//      (one byte per query head and key, two for d = 256: the later launches
+//      and the attention pass read them instead of the d/8-byte sign rows),
+//      and per key chunk a histogram of the keys' top 11 bits;
+//   2. pick_kernel: per (b, head), sums the chunk histograms and picks the
+//      bucket (top-11-bit digit) holding the k-th largest key; `remain` keys
+//      are still to be taken from it;
+//   3. collect_kernel: lists the keys of that bucket (about 4% of a head's
+//      keys at k = S/10 on Gaussian data), each as one 32-bit entry holding
+//      key bits 20..6 and the index in its chunk;
+//   4. final_kernel: per (b, head), an exact radix select of the remain-th
+//      largest listed key (T; `need` keys equal to T are taken), then the
+//      need-th smallest index among the listed keys equal to T (ties are
+//      taken lowest index first) as the cutoff.
+// The attention kernel selects key > T, or key == T at an index <= cutoff.
 //
-// The first pass computes the popcounts from the K sign planes and stores
-// them (one byte per query head and key; two for d = 256), so the later
-// passes, the tie scan and the attention pass read those instead of the
-// d/8-byte sign rows.
+// Why key bits 20..6 identify a listed key: with a finite fp16 scale the
+// score is an exact fp32 product of an 11-bit significand and an even integer
+// of magnitude <= 256 (at most 18 significant bits), so its low 6 bits are
+// zero, as are those of +-inf and +0.  The ordered key therefore ends in six
+// 0 bits when bit 31 is set (scores >= +0) and in six 1 bits otherwise (the
+// key of a negative score is the complement; NaN ranks as -inf).  Listed keys
+// share bits 31..21 (the bucket), which fixes the rest.
+//
+// Scores are compared as exact floats against bounds derived from the key
+// prefix (see key_floor), which order like the keys; a wave holding a
+// non-finite scale compares the keys themselves.
 //
 // Workspace: chunk histograms [B*Hq][nsplit][2048] u32 | prefix [B*Hq] u32
-//            | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G] | attention partials.
+//   | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G]
+//   | bucket lists [B*Hq][nsplit][4 waves][wcap] u32 | list counts [B*Hq][nsplit][4] u32
+//   | attention partials.
 #include "attn.h"
 
 namespace {
@@ -29,17 +42,26 @@ using bc::PcPack;
 using bc::PcT;
 
 constexpr int kBins = 2048;
+constexpr int kMaxSplit = 1024;       // key chunks per head
+constexpr int kMaxChunk = 65536;      // keys per chunk (16-bit indices in the lists)
+constexpr int kFinalThreads = 512;
+constexpr int kStageCap = 6144;       // bucket entries the final select holds in LDS
+                                      // (more: re-read from the lists each round)
+static_assert(kStageCap % kFinalThreads == 0 && kFinalThreads <= kBins, "final select sizes");
 
 struct SelArgs {
     const uint16_t* q;
     BinPlanes kb;
     int Hq, Hkv, S, kv_stride;
-    int nsplit, chunk;   // key chunks of the histogram passes
-    uint32_t* hist;      // [B*Hq][nsplit][2048] each key chunk's histogram of a pass
-    uint32_t* prefix;    // [B*Hq]
-    int32_t* remain;     // [B*Hq]
+    int nsplit, chunk;   // key chunks of the passes (chunk: a multiple of 64, <= kMaxChunk)
+    int wcap;            // list entries per (head, chunk, wave)
+    uint32_t* hist;      // [B*Hq][nsplit][2048] each key chunk's top-digit histogram
+    uint32_t* prefix;    // [B*Hq] bucket digit << 21, then the threshold T
+    int32_t* remain;     // [B*Hq] keys still to take from the bucket, then at T
     int32_t* cutoff;     // [B*Hq]
     void* pcs;           // [B*Hq/G][pcs_stride(S)][G] popcounts (PcT<D>)
+    uint32_t* lists;     // [B*Hq][nsplit][4][wcap] bucket entries
+    uint32_t* counts;    // [B*Hq][nsplit][4] entries per list region
     int oct;             // K scales load eight keys at a time (kv_stride % 8 == 0,
                          // 16-byte aligned scale plane)
 };
@@ -67,127 +89,267 @@ __device__ __forceinline__ uint32_t key_of_pc(int pc, float sk) {
     return ordered_key(sk * (float)(2 * pc - D));
 }
 
-// Histogram of digit `pass` over keys matching prefix[bhq] in the higher digits.
-// grid: (splits, B*Hkv*(group/G)); block 256; each thread strides over keys.
+// Every key of a chunk: the popcounts of the G heads of the group (stored)
+// and each head's histogram of the top 11 key bits, stored whole for the
+// chunk (plain coalesced stores; the pick sums the chunks).
+// grid: (nsplit, B*Hkv*(group/G)); block 256.
 template <int D, int G>
-__global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chunk) {
+__global__ __launch_bounds__(256) void hist_kernel(SelArgs a) {
     __shared__ uint32_t qs[G][D / 32];
     __shared__ uint32_t h[G][kBins];
     const int nqg = (a.Hq / a.Hkv) / G;
     const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
     const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
-    if (pass == 0) load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
+    load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
     for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) (&h[0][0])[i] = 0u;
     __syncthreads();
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 0x3FFu : 0x7FFu;
-    const int pbits = pass == 0 ? 0 : (pass == 1 ? 11 : 22);
-    uint32_t pref[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) pref[g] = pass == 0 ? 0u : a.prefix[bhq0 + g];
     const int64_t base = (int64_t)bkv * a.kv_stride;
-    const int k0 = blockIdx.x * chunk, k1 = min(a.S, k0 + chunk);
+    const int k0 = blockIdx.x * a.chunk, k1 = min(a.S, k0 + a.chunk);
     using P = PcT<D>;
     using Pack = PcPack<P, G>;
     Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S);   // this group's packs
-    // the prefix found so far as a key range [klo, khi] and, for scores of a
-    // finite scale, as the float range (flo, fhi]
-    uint32_t klo[G], khi[G];
-    float flo[G], fhi[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        const uint32_t low = pbits == 0 ? 0xFFFFFFFFu : (0xFFFFFFFFu >> pbits);
-        klo[g] = pref[g] & ~low;
-        khi[g] = klo[g] | low;
-        flo[g] = klo[g] == 0u ? -INFINITY : key_floor(klo[g] - 1u);
-        fhi[g] = key_floor(khi[g]);
-    }
-    // one key: the popcounts pc[g] of the G heads and the K scale
-    auto count_key = [&](const int* pc, float sk, bool all) {
+    auto count = [&](const Pack& pk, float sk) {
         // (a wave with a non-finite scale takes the key path for all its lanes)
         if (__ballot(!finite_scale(sk)) == 0ull) {
             const float sk2 = 2.0f * sk, nd = -(float)D * sk;
-            float sc[G];
-            bool mt[G];
-            bool any = false;
+#pragma unroll
+            for (int g = 0; g < G; g++) atomicAdd(&h[g][ordered_bits(fmaf((float)pk.v[g], sk2, nd)) >> 21], 1u);
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; g++) atomicAdd(&h[g][key_of_pc<D>((int)pk.v[g], sk) >> 21], 1u);
+        }
+    };
+    // Two register stages of UP keys per thread: the loads of the next stage
+    // are in flight while a stage is counted.
+    constexpr int UP = D >= 256 ? 2 : 4;
+    constexpr int step = UP * 256;
+    struct Stage {
+        SignWords<D> ks[UP];
+        uint16_t sk[UP];
+    };
+    auto load = [&](Stage& st, int s) {
+#pragma unroll
+        for (int u = 0; u < UP; u++) {
+            const int ss = s + u * 256;
+            const int64_t i = base + (ss < k1 ? ss : k0);
+            st.ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
+            st.sk[u] = a.kb.scales[i];
+        }
+    };
+    auto run = [&](const Stage& st, int s) {
+#pragma unroll
+        for (int u = 0; u < UP; u++) {
+            const int ss = s + u * 256;
+            if (ss >= k1) break;
+            Pack pk;
+#pragma unroll
+            for (int g = 0; g < G; g++) pk.v[g] = (P)popc_of<D>(qs[g], st.ks[u]);
+            pcs[ss] = pk;
+            count(pk, h2f(st.sk[u]));
+        }
+    };
+    if (k0 + (int)threadIdx.x < k1) {
+        Stage sa, sb;
+        int s = k0 + threadIdx.x;
+        load(sa, s);
+        for (;;) {
+            load(sb, s + step);
+            run(sa, s);
+            s += step;
+            if (s >= k1) break;
+            load(sa, s + step);
+            run(sb, s);
+            s += step;
+            if (s >= k1) break;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) {
+        const int g = i / kBins, bin = i % kBins;
+        a.hist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * kBins + bin] = h[g][bin];
+    }
+}
+
+// One block per (b, query head): sum the chunk histograms and pick the bucket
+// (top-11-bit digit) holding the top_k-th largest key: prefix = digit << 21,
+// remain = top_k - (keys above the bucket).
+__global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int top_k) {
+    __shared__ uint32_t cnt[kBins];
+    __shared__ uint32_t part[256];
+    const int bhq = blockIdx.x;
+    const uint32_t* h = a.hist + (int64_t)bhq * a.nsplit * kBins;
+    {
+        // eight consecutive bins per thread
+        const int b0 = threadIdx.x * 8;
+        uint32_t sum[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        for (int c = 0; c < a.nsplit; c++) {
+            const bc_v4u x = *(const bc_v4u*)(h + (int64_t)c * kBins + b0);
+            const bc_v4u y = *(const bc_v4u*)(h + (int64_t)c * kBins + b0 + 4);
+            sum[0] += x[0]; sum[1] += x[1]; sum[2] += x[2]; sum[3] += x[3];
+            sum[4] += y[0]; sum[5] += y[1]; sum[6] += y[2]; sum[7] += y[3];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) cnt[b0 + j] = sum[j];
+    }
+    __syncthreads();
+    const int remain = top_k;
+    // per-thread counts of 8 consecutive bins (descending digits)
+    constexpr int per = kBins / 256;
+    uint32_t local = 0;
+    for (int j = 0; j < per; j++) local += cnt[kBins - 1 - (threadIdx.x * per + j)];
+    part[threadIdx.x] = local;
+    __syncthreads();
+    if (remain <= 0) {
+        if (threadIdx.x == 0) {
+            a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
+            a.remain[bhq] = 0;
+        }
+        return;
+    }
+    // inclusive prefix over the 256 partial counts (Hillis-Steele in LDS)
+    uint32_t incl = local;
+    for (int off = 1; off < 256; off <<= 1) {
+        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
+        __syncthreads();
+        incl += add;
+        part[threadIdx.x] = incl;
+        __syncthreads();
+    }
+    const uint32_t excl = incl - local;
+    if (threadIdx.x == 255 && incl < (uint32_t)remain) {
+        // fewer keys than remain: select everything
+        a.prefix[bhq] = 0u;
+        a.remain[bhq] = 0;
+    }
+    if (excl < (uint32_t)remain && incl >= (uint32_t)remain) {
+        // this thread's 8 bins hold the remain-th largest key
+        uint32_t above = excl;
+        int digit = 0;
+        for (int j = 0; j < per; j++) {
+            const int d = kBins - 1 - (threadIdx.x * per + j);
+            if (above + cnt[d] >= (uint32_t)remain) {
+                digit = d;
+                break;
+            }
+            above += cnt[d];
+        }
+        a.prefix[bhq] = (uint32_t)digit << 21;
+        a.remain[bhq] = remain - (int)above;
+    }
+}
+
+// List regions: each (head, chunk) has one region of wcap entries per wave
+// of the collecting workgroup; a wave sees at most 64 lanes x ceil(octets /
+// 256) octets of its chunk (plain path: 64 x ceil(keys / 256) keys), which is
+// at most 512 * ceil(chunk / 2048) keys, and never more than the chunk.
+inline int list_wave_cap(int chunk) {
+    const int c = 512 * ((chunk + 2047) / 2048);
+    return c < chunk ? c : chunk;
+}
+
+// Orders a wave's LDS writes before its later LDS reads of other lanes' data.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The bucket lists: every key of the chunk whose top 11 bits are the picked
+// bucket of a head goes into that head's list as
+// (key bits 20..6) << 16 | (index - chunk start).  A wave gathers the entries
+// of a row of 512 keys in its LDS area (ballot counts, no atomics), then
+// appends them to its own list region with whole-wave stores, so a row costs
+// one store per head instead of one per key step and head; it stores its
+// region counts at the end.  Every lane of a wave runs the same trip count
+// (lanes past the chunk take no key).
+// OCT: the eight-key loads (SelArgs::oct); one path per instance keeps the
+// loop's code within the instruction cache.
+// grid: (nsplit, B*Hkv*(group/G)); block 256.
+template <int D, int G, bool OCT>
+__global__ __launch_bounds__(256) void collect_kernel(SelArgs a) {
+    constexpr int kRow = 512;   // keys of a wave's row (64 lanes x 8)
+    __shared__ uint32_t stg[4][G][kRow];
+    const int nqg = (a.Hq / a.Hkv) / G;
+    const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
+    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+    const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
+    const int wave = threadIdx.x >> 6;
+    const int64_t base = (int64_t)bkv * a.kv_stride;
+    const int k0 = blockIdx.x * a.chunk, k1 = min(a.S, k0 + a.chunk);
+    using P = PcT<D>;
+    using Pack = PcPack<P, G>;
+    const Pack* pcs = (const Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S);
+    // the bucket as a key range [klo, khi] and, for scores of a finite scale,
+    // as the float range (flo, fhi]
+    uint32_t klo[G], khi[G];
+    float flo[G], fhi[G];
+    bool live[G];
+    uint32_t* lst[G];
+    uint32_t off[G];   // entries in the wave's list region
+    uint32_t rc[G];    // entries of the current row in LDS
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int bhq = bhq0 + g;
+        live[g] = a.remain[bhq] > 0;
+        klo[g] = a.prefix[bhq] & 0xFFE00000u;
+        khi[g] = klo[g] | 0x001FFFFFu;
+        flo[g] = klo[g] == 0u ? -INFINITY : key_floor(klo[g] - 1u);
+        fhi[g] = key_floor(khi[g]);
+        lst[g] = a.lists + (((int64_t)bhq * a.nsplit + blockIdx.x) * 4 + wave) * a.wcap;
+        off[g] = 0u;
+        rc[g] = 0u;
+    }
+    // one key: the popcounts pc[g] of the G heads, the K scale, the index
+    auto take = [&](const int* pc, float sk, int s, bool valid) {
+        bool mt[G];
+        uint32_t key[G];
+        if (__ballot(valid && !finite_scale(sk)) == 0ull) {
+            const float sk2 = 2.0f * sk, nd = -(float)D * sk;
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                sc[g] = fmaf((float)pc[g], sk2, nd);
-                mt[g] = all || (sc[g] > flo[g] && sc[g] <= fhi[g]);
-                any = any || mt[g];
-            }
-            // (later passes: most waves have no match for a key, and skip it)
-            if (all || __ballot(any) != 0ull) {
-#pragma unroll
-                for (int g = 0; g < G; g++)
-                    if (mt[g]) atomicAdd(&h[g][(ordered_bits(sc[g]) >> shift) & dmask], 1u);
+                const float sc = fmaf((float)pc[g], sk2, nd);
+                mt[g] = valid && live[g] && sc > flo[g] && sc <= fhi[g];
+                key[g] = ordered_bits(sc);
             }
         } else {
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const uint32_t key = key_of_pc<D>(pc[g], sk);
-                if (key >= klo[g] && key <= khi[g]) atomicAdd(&h[g][(key >> shift) & dmask], 1u);
+                key[g] = key_of_pc<D>(pc[g], sk);
+                mt[g] = valid && live[g] && key[g] >= klo[g] && key[g] <= khi[g];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const uint64_t m = __ballot(mt[g]);
+            if (m != 0ull) {
+                if (mt[g]) {
+                    const uint32_t below =
+                        __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                    stg[wave][g][rc[g] + below] = (((key[g] >> 6) & 0x7FFFu) << 16) | (uint32_t)(s - k0);
+                }
+                rc[g] += (uint32_t)__builtin_popcountll(m);
             }
         }
     };
-    auto count = [&](const Pack& pk, float sk, bool all) {
-        int pc[G];
+    // the row's entries from LDS to the list regions
+    auto flush = [&]() {
+        wave_lds_sync();
 #pragma unroll
-        for (int g = 0; g < G; g++) pc[g] = (int)pk.v[g];
-        count_key(pc, sk, all);
-    };
-    if (pass == 0) {
-        // popcounts from the sign rows, stored for the later passes.  Two
-        // register stages of UP keys per thread: the loads of the next stage
-        // are in flight while a stage is counted.
-        constexpr int UP = D >= 256 ? 2 : 4;
-        constexpr int step = UP * 256;
-        struct Stage {
-            SignWords<D> ks[UP];
-            uint16_t sk[UP];
-        };
-        auto load = [&](Stage& st, int s) {
-#pragma unroll
-            for (int u = 0; u < UP; u++) {
-                const int ss = s + u * 256;
-                const int64_t i = base + (ss < k1 ? ss : k0);
-                st.ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
-                st.sk[u] = a.kb.scales[i];
-            }
-        };
-        auto run = [&](const Stage& st, int s) {
-#pragma unroll
-            for (int u = 0; u < UP; u++) {
-                const int ss = s + u * 256;
-                if (ss >= k1) break;
-                Pack pk;
-#pragma unroll
-                for (int g = 0; g < G; g++) pk.v[g] = (P)popc_of<D>(qs[g], st.ks[u]);
-                pcs[ss] = pk;
-                count(pk, h2f(st.sk[u]), true);
-            }
-        };
-        if (k0 + (int)threadIdx.x < k1) {
-            Stage sa, sb;
-            int s = k0 + threadIdx.x;
-            load(sa, s);
-            for (;;) {
-                load(sb, s + step);
-                run(sa, s);
-                s += step;
-                if (s >= k1) break;
-                load(sa, s + step);
-                run(sb, s);
-                s += step;
-                if (s >= k1) break;
-            }
+        for (int g = 0; g < G; g++) {
+            for (uint32_t i = lane; i < rc[g]; i += 64) lst[g][off[g] + i] = stg[wave][g][i];
+            off[g] += rc[g];
+            rc[g] = 0u;
         }
-    } else if (a.oct) {
-        // stored popcounts, eight consecutive keys per lane and load: their
-        // packs (8 G-head packs, whole 16-byte loads where they fill one) and
-        // their K scales (16 bytes).  Two register stages of UP octets: the
-        // loads of the next stage are in flight while a stage is counted.
+        wave_lds_sync();
+    };
+    if constexpr (OCT) {
+        // eight consecutive keys per lane and load: their packs (whole 16-byte
+        // loads where they fill one) and their K scales (16 bytes); two
+        // register stages of UP octets, the next stage's loads in flight
+        // while a stage is taken (one copy of the stage body: the next stage
+        // moves into the current one)
         constexpr int kOct = 8 * (int)sizeof(Pack);   // pack bytes of eight keys
         constexpr int NW = kOct / 4;
         constexpr int UP = kOct >= 64 ? 1 : 2;         // octets per lane and stage
@@ -222,10 +384,9 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
 #pragma unroll
             for (int u = 0; u < UP; u++) {
                 const int oo = o + u * 256;
-                if (oo >= o1) break;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    if (8 * oo + j >= k1) break;   // (only the range's last octet is partial)
+                    const int s = 8 * oo + j;
                     const uint32_t sw = st.sc[u][j >> 1];
                     const float sk = h2f((uint16_t)((j & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
                     int pc[G];
@@ -235,224 +396,310 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a, int pass, int chun
                         const int byte = (j * G + g) * pb;
                         pc[g] = (int)((st.pw[u][byte / 4] >> (8 * (byte % 4))) & ((1u << (8 * pb)) - 1u));
                     }
-                    count_key(pc, sk, false);
+                    take(pc, sk, s, oo < o1 && s < k1);
                 }
+                flush();
             }
         };
-        Stage sa, sb;
-        int o = o0 + threadIdx.x;
-        load(sa, o);
+        Stage cur, nxt;
+        int o = o0 + threadIdx.x;      // this lane's octet of the stage
+        int ow = o0 + 64 * wave;       // the wave's first octet of the stage (uniform)
+        load(cur, o);
         for (;;) {
-            load(sb, o + step);
-            run(sa, o);
+            load(nxt, o + step);
+            run(cur, o);
             o += step;
-            if (o >= o1) break;
-            load(sa, o + step);
-            run(sb, o);
-            o += step;
-            if (o >= o1) break;
+            ow += step;
+            if (ow >= o1) break;
+            cur = nxt;
         }
     } else {
-        // stored popcounts: sixteen keys per thread per iteration
+        // sixteen keys per thread per iteration
         constexpr int U = 16;
-        for (int s = k0 + threadIdx.x; s < k1; s += U * blockDim.x) {
+        for (int sw = k0 + 64 * wave; sw < k1; sw += U * 256) {   // the wave's first key (uniform)
+            const int s = sw - 64 * wave + (int)threadIdx.x;
             Pack pk[U];
             float sk[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int ss = s + u * blockDim.x;
-                const int sc = ss < k1 ? ss : s;
+                const int ss = s + u * 256;
+                const int sc = ss < k1 ? ss : k0;
                 pk[u] = pcs[sc];
                 sk[u] = h2f(a.kb.scales[base + sc]);
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                if (s + u * (int)blockDim.x >= k1) break;
-                count(pk[u], sk[u], false);
+                const int ss = s + u * 256;
+                int pc[G];
+#pragma unroll
+                for (int g = 0; g < G; g++) pc[g] = (int)pk[u].v[g];
+                take(pc, sk[u], ss, ss < k1);
+                if (u % 8 == 7) flush();   // (a row: 8 keys per lane)
             }
         }
     }
-    __syncthreads();
-    // this chunk's histogram, stored whole (plain coalesced stores; the pick
-    // sums the chunks, and the last pass's chunk histograms locate the ties)
-    const int nb = pass == 2 ? 1024 : kBins;
-    for (int i = threadIdx.x; i < G * nb; i += blockDim.x) {
-        const int g = i / nb, bin = i % nb;
-        a.hist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * kBins + bin] = h[g][bin];
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+            a.counts[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * 4 + wave] = off[g];
     }
 }
 
-// One block per (b, query head): sum the chunk histograms of the pass and
-// pick the digit holding the remain-th largest key; extend the prefix.
-__global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int pass, int top_k) {
-    __shared__ uint32_t cnt[kBins];
-    __shared__ uint32_t part[256];
-    const int bhq = blockIdx.x;
-    const uint32_t* h = a.hist + (int64_t)bhq * a.nsplit * kBins;
-    const int nbins = pass == 2 ? 1024 : 2048;
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    {
-        // eight consecutive bins per thread (the last pass stores 1024)
-        const int b0 = threadIdx.x * 8;
-        uint32_t sum[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        if (b0 < nbins) {
-            for (int c = 0; c < a.nsplit; c++) {
-                const bc_v4u x = *(const bc_v4u*)(h + (int64_t)c * kBins + b0);
-                const bc_v4u y = *(const bc_v4u*)(h + (int64_t)c * kBins + b0 + 4);
-                sum[0] += x[0]; sum[1] += x[1]; sum[2] += x[2]; sum[3] += x[3];
-                sum[4] += y[0]; sum[5] += y[1]; sum[6] += y[2]; sum[7] += y[3];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) cnt[b0 + j] = sum[j];
+// Inclusive sum of v over the block's NT threads (wsum: LDS [NT / 64]).
+template <int NT>
+__device__ uint32_t block_incl_sum(uint32_t v, uint32_t* wsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t up = __shfl_up(v, off, 64);
+        if (lane >= off) v += up;
     }
+    if (lane == 63) wsum[wave] = v;
     __syncthreads();
-    int remain = pass == 0 ? top_k : a.remain[bhq];
-    uint32_t prefix = pass == 0 ? 0u : a.prefix[bhq];
-    // per-thread counts of 8 consecutive bins (descending digits)
-    const int per = kBins / 256;
+    uint32_t base = 0;
+    for (int w = 0; w < wave; w++) base += wsum[w];
+    __syncthreads();   // (wsum is free again)
+    return v + base;
+}
+
+// Given the histogram cnt[nb] of the elements' digits, the digit d of the
+// r-th largest element (1 <= r <= total): count(digit > d) < r <=
+// count(digit >= d).  Every thread gets d and count(digit > d).
+template <int NT>
+__device__ void block_pick(const uint32_t* cnt, int nb, uint32_t r, uint32_t* wsum, uint32_t* res, int& digit,
+                           uint32_t& above) {
+    const int per = (nb + NT - 1) / NT;   // consecutive bins per thread, descending
     uint32_t local = 0;
     for (int j = 0; j < per; j++) {
-        const int d = nbins - 1 - (threadIdx.x * per + j);
+        const int d = nb - 1 - ((int)threadIdx.x * per + j);
         if (d >= 0) local += cnt[d];
     }
-    part[threadIdx.x] = local;
-    __syncthreads();
-    if (remain <= 0) {
-        if (threadIdx.x == 0 && pass == 0) {
-            a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
-            a.remain[bhq] = 0;
-        }
-        return;
+    if (threadIdx.x == 0) {
+        res[0] = 0u;   // (r beyond the total: digit 0, nothing above)
+        res[1] = 0u;
     }
-    // inclusive prefix over the 256 partial counts (Hillis-Steele in LDS)
-    uint32_t incl = local;
-    for (int off = 1; off < 256; off <<= 1) {
-        const uint32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
-        __syncthreads();
-        incl += add;
-        part[threadIdx.x] = incl;
-        __syncthreads();
-    }
+    const uint32_t incl = block_incl_sum<NT>(local, wsum);
     const uint32_t excl = incl - local;
-    if (threadIdx.x == 255 && incl < (uint32_t)remain) {
-        // fewer matching keys than remain: select everything
-        a.prefix[bhq] = 0u;
-        a.remain[bhq] = 0;
-    }
-    if (excl < (uint32_t)remain && incl >= (uint32_t)remain) {
-        // this thread's 8 bins hold the remain-th largest key
-        uint32_t above = excl;
-        int digit = 0;
+    if (excl < r && incl >= r) {
+        uint32_t ab = excl;
+        int dg = 0;
         for (int j = 0; j < per; j++) {
-            const int d = nbins - 1 - (threadIdx.x * per + j);
+            const int d = nb - 1 - ((int)threadIdx.x * per + j);
             if (d < 0) break;
-            if (above + cnt[d] >= (uint32_t)remain) {
-                digit = d;
+            if (ab + cnt[d] >= r) {
+                dg = d;
                 break;
             }
-            above += cnt[d];
+            ab += cnt[d];
         }
-        a.prefix[bhq] = prefix | ((uint32_t)digit << shift);
-        a.remain[bhq] = remain - (int)above;
+        res[0] = (uint32_t)dg;
+        res[1] = ab;
     }
+    __syncthreads();
+    digit = (int)res[0];
+    above = res[1];
+    __syncthreads();   // (res is free again)
 }
 
-// Cutoff index of the ties at the final threshold T: one block per (b, query
-// head).  The chunk histograms give the chunk holding the need-th tie; that
-// chunk is scanned from the stored popcounts and K scales (see below).
-template <int D, int G>
-__global__ __launch_bounds__(256) void tie_locate_kernel(SelArgs a) {
-    __shared__ int sh_chunk, sh_rank, sh_total;
-    __shared__ uint64_t tmask[64][4];   // [stripe][wave] tie ballots of a window
-    using Pack = PcPack<PcT<D>, G>;
+// One block per (b, query head): the exact threshold and tie cutoff from the
+// head's bucket list.  The list regions are read in one flat index space
+// (region = chunk * 4 + wave); when the bucket fits in LDS it is staged there
+// once, else every round re-reads it.
+__global__ __launch_bounds__(kFinalThreads) void final_kernel(SelArgs a) {
+    constexpr int NT = kFinalThreads;
+    __shared__ uint32_t s_k[kStageCap];        // key bits 20..6
+    __shared__ uint32_t s_i[kStageCap];        // key index
+    __shared__ uint32_t cnt[kBins];
+    __shared__ uint32_t rpre[4 * kMaxSplit + 1];
+    __shared__ uint32_t wsum[NT / 64];
+    __shared__ uint32_t res[2];
     const int bhq = blockIdx.x;
-    const int b = bhq / a.Hq, h = bhq % a.Hq;
-    const int kvh = h / (a.Hq / a.Hkv);
-    const int g = bhq % G;   // head slot in its group (groups are G consecutive heads)
-    const int need = a.remain[bhq];
-    if (need <= 0) {
+    const int r0 = a.remain[bhq];
+    if (r0 <= 0) {
+        // k = 0, or every key taken: the prefix already says which; no ties
         if (threadIdx.x == 0) a.cutoff[bhq] = -1;
         return;
     }
-    const uint32_t T = a.prefix[bhq];
-    const float tv = key_value(T);   // the score of key T (finite scales)
-    if (threadIdx.x == 0) {
-        const uint32_t* ch = a.hist + (int64_t)bhq * a.nsplit * kBins + (T & 0x3FFu);
-        int cum = 0, c = 0;
-        for (; c < a.nsplit - 1; c++) {
-            const int t = (int)ch[(int64_t)c * kBins];
-            if (cum + t >= need) break;
-            cum += t;
-        }
-        sh_chunk = c;
-        sh_rank = need - cum;   // the rank-th tie (from 1) of chunk c is the last one taken
-    }
-    __syncthreads();
-    const int64_t base = ((int64_t)b * a.Hkv + kvh) * a.kv_stride;
-    const Pack* pcs = (const Pack*)a.pcs + (int64_t)(bhq - g) / G * bc::pcs_stride(a.S);
-    const int k0 = sh_chunk * a.chunk, k1 = min(a.S, k0 + a.chunk);
-    // windows of 64 stripes of 256 keys, read coalesced (all loads of 16
-    // stripes issued first); a wave ballot per stripe records the ties; one
-    // wave prefix-sums the 64 stripe counts, finds the stripe holding the
-    // rank-th tie, and picks the key from that stripe's per-wave masks
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int rank = sh_rank;
-    for (int w0 = k0; w0 < k1; w0 += 256 * 64) {
-        for (int b0 = 0; b0 < 64; b0 += 16) {
-            int pcv[16];
-            float skv[16];
+    const uint32_t P0 = a.prefix[bhq];
+    const int nreg = 4 * a.nsplit;
+    const uint32_t* counts = a.counts + (int64_t)bhq * nreg;
+    const uint32_t* lists = a.lists + (int64_t)bhq * nreg * a.wcap;
+    {
+        // exclusive prefix of the region counts
+        constexpr int kPer = 4 * kMaxSplit / NT;
+        uint32_t c[kPer];
+        uint32_t local = 0;
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const int sv = w0 + (b0 + u) * 256 + (int)threadIdx.x;
-                const int sc = sv < k1 ? sv : k0;
-                pcv[u] = (int)pcs[sc].v[g];
-                skv[u] = h2f(a.kb.scales[base + sc]);
-            }
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const int sv = w0 + (b0 + u) * 256 + (int)threadIdx.x;
-                const float sk = skv[u];
-                bool tie;
-                if (__ballot(!finite_scale(sk)) == 0ull) tie = fmaf((float)pcv[u], 2.0f * sk, -(float)D * sk) == tv;
-                else tie = key_of_pc<D>(pcv[u], sk) == T;
-                const uint64_t m = __ballot(sv < k1 && tie);
-                if (lane == 0) tmask[b0 + u][wave] = m;
-            }
+        for (int j = 0; j < kPer; j++) {
+            const int r = (int)threadIdx.x * kPer + j;
+            c[j] = r < nreg ? counts[r] : 0u;
+            local += c[j];
         }
+        const uint32_t incl = block_incl_sum<NT>(local, wsum);
+        uint32_t run = incl - local;
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const int r = (int)threadIdx.x * kPer + j;
+            if (r < nreg) rpre[r] = run;
+            run += c[j];
+        }
+        if (threadIdx.x == NT - 1) rpre[nreg] = incl;
         __syncthreads();
-        if (wave == 0) {
-            const int j = lane;   // stripe
-            const uint32_t c = (uint32_t)(__builtin_popcountll(tmask[j][0]) + __builtin_popcountll(tmask[j][1]) +
-                                          __builtin_popcountll(tmask[j][2]) + __builtin_popcountll(tmask[j][3]));
-            uint32_t incl = c;
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t up = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += up;
-            }
-            const uint32_t excl = incl - c;
-            if (excl < (uint32_t)rank && incl >= (uint32_t)rank) {
-                uint32_t r = (uint32_t)rank - excl;
-                for (int w = 0; w < 4; w++) {
-                    const uint64_t m = tmask[j][w];
-                    const uint32_t cw = (uint32_t)__builtin_popcountll(m);
-                    if (r <= cw) {
-                        for (int i = 0; i < 64; i++) {
-                            if (((m >> i) & 1ull) && --r == 0) {
-                                a.cutoff[bhq] = w0 + j * 256 + w * 64 + i;
-                                break;
-                            }
-                        }
-                        break;
-                    }
-                    r -= cw;
+    }
+    const uint32_t n = rpre[nreg];
+    // entry i of the flat list: its region is the last r with rpre[r] <= i;
+    // returns (key bits 20..6) and the key index
+    auto fetch = [&](uint32_t i, uint32_t& k15, uint32_t& idx) {
+        int lo = 0, hi = nreg - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (rpre[mid] <= i) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t e = lists[(int64_t)lo * a.wcap + (i - rpre[lo])];
+        k15 = e >> 16;
+        idx = (uint32_t)(lo >> 2) * (uint32_t)a.chunk + (e & 0xFFFFu);
+    };
+    constexpr int U = 8;   // entries per thread with their loads in flight together
+    const bool staged = n <= (uint32_t)kStageCap;
+    if (staged) {
+        // each thread a run of E <= kStageCap / NT consecutive entries: the
+        // region of its first entry by binary search, then walking forward
+        // (the next region's start kept in a register), so the loads issue
+        // back to back
+        constexpr int EM = kStageCap / NT;
+        const uint32_t E = (n + NT - 1) / NT;
+        const uint32_t i0 = threadIdx.x * E;
+        if (i0 < n) {
+            int rg = 0;
+            {
+                int hi = nreg - 1;
+                while (rg < hi) {
+                    const int mid = (rg + hi + 1) >> 1;
+                    if (rpre[mid] <= i0) rg = mid;
+                    else hi = mid - 1;
                 }
             }
-            if (lane == 63) sh_total = (int)incl;
+            uint32_t nxt = rpre[rg + 1];
+            uint32_t e[EM];
+            int rgs[EM];
+#pragma unroll
+            for (int u = 0; u < EM; u++) {
+                const uint32_t i = i0 + u;
+                if ((uint32_t)u < E && i < n) {
+                    while (i >= nxt) {   // (past the last entry of region rg; empty regions skipped)
+                        rg++;
+                        nxt = rpre[rg + 1];
+                    }
+                    rgs[u] = rg;
+                    e[u] = lists[(int64_t)rg * a.wcap + (i - rpre[rg])];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < EM; u++) {
+                const uint32_t i = i0 + u;
+                if ((uint32_t)u < E && i < n) {
+                    s_k[i] = e[u] >> 16;
+                    s_i[i] = (uint32_t)(rgs[u] >> 2) * (uint32_t)a.chunk + (e[u] & 0xFFFFu);
+                }
+            }
         }
         __syncthreads();
-        if (sh_total >= rank) break;   // found in this window
-        rank -= sh_total;
+    }
+    // fn(key bits 20..6, index) for every entry of the bucket
+    auto each = [&](auto&& fn) {
+        if (staged) {
+            for (uint32_t i = threadIdx.x; i < n; i += NT) fn(s_k[i], s_i[i]);
+        } else {
+            for (uint32_t i0 = 0; i0 < n; i0 += NT * U) {
+                uint32_t k[U], x[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const uint32_t i = i0 + u * NT + threadIdx.x;
+                    if (i < n) fetch(i, k[u], x[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const uint32_t i = i0 + u * NT + threadIdx.x;
+                    if (i < n) fn(k[u], x[u]);
+                }
+            }
+        }
+    };
+    // The r-th largest of val(k, x) < 2^vbits (vbits <= 31) over the entries
+    // with part(k, x), by radix rounds of up to 11 bits from the top.  On
+    // return r is what remains of it at that value (the number of entries
+    // equal to it to take) and t the number of such entries.
+    auto select = [&](uint32_t& r, int vbits, auto&& val, auto&& part, uint32_t& t) -> uint32_t {
+        uint32_t pref = 0;
+        int hi = vbits;   // value bits above hi are decided
+        int d = 0;
+        while (hi > 0) {
+            const int nbits = hi >= 11 ? 11 : hi;
+            const int shift = hi - nbits;
+            const int nb = 1 << nbits;
+            for (int i = threadIdx.x; i < nb; i += NT) cnt[i] = 0u;
+            __syncthreads();
+            each([&](uint32_t k, uint32_t x) {
+                if (!part(k, x)) return;
+                const uint32_t v = val(k, x);
+                if ((v >> hi) == (pref >> hi)) atomicAdd(&cnt[(v >> shift) & (uint32_t)(nb - 1)], 1u);
+            });
+            __syncthreads();
+            uint32_t above;
+            block_pick<NT>(cnt, nb, r, wsum, res, d, above);
+            pref |= (uint32_t)d << shift;
+            r -= above;
+            hi = shift;
+        }
+        t = cnt[d];
+        __syncthreads();   // (cnt is free again)
+        return pref;
+    };
+    uint32_t r = (uint32_t)r0, t = 0;
+    const uint32_t kT = select(
+        r, 15, [](uint32_t k, uint32_t) { return k; }, [](uint32_t, uint32_t) { return true; }, t);
+    const uint32_t T = (P0 & 0xFFE00000u) | (kT << 6) | ((P0 & 0x80000000u) ? 0u : 0x3Fu);
+    const uint32_t need = r;   // 1 <= need <= t
+    int cutoff;
+    if (need >= t) {
+        // every key equal to T is taken: the cutoff is the largest such index
+        if (threadIdx.x == 0) res[0] = 0u;
+        __syncthreads();
+        each([&](uint32_t k, uint32_t x) {
+            if (k == kT) atomicMax(&res[0], x);
+        });
+        __syncthreads();
+        cutoff = (int)res[0];
+    } else if (t <= (uint32_t)NT) {
+        // a few ties: their indices compacted in LDS (cnt is free); the one
+        // with need - 1 smaller indices is the cutoff
+        if (threadIdx.x == 0) res[0] = 0u;
+        __syncthreads();
+        each([&](uint32_t k, uint32_t x) {
+            if (k == kT) cnt[atomicAdd(&res[0], 1u)] = x;
+        });
+        __syncthreads();
+        if (threadIdx.x < t) {
+            const uint32_t x = cnt[threadIdx.x];
+            uint32_t below = 0;
+            for (uint32_t j = 0; j < t; j++) below += cnt[j] < x ? 1u : 0u;
+            if (below == need - 1) res[1] = x;
+        }
+        __syncthreads();
+        cutoff = (int)res[1];
+    } else {
+        // many ties: the need-th smallest index is the need-th largest of
+        // 0x7FFFFFFF - index
+        uint32_t rr = need, tt = 0;
+        const uint32_t v = select(
+            rr, 31, [](uint32_t, uint32_t x) { return 0x7FFFFFFFu - x; },
+            [kT](uint32_t k, uint32_t) { return k == kT; }, tt);
+        cutoff = (int)(0x7FFFFFFFu - v);
+    }
+    if (threadIdx.x == 0) {
+        a.prefix[bhq] = T;
+        a.remain[bhq] = (int)need;
+        a.cutoff[bhq] = cutoff;
     }
 }
 
@@ -467,12 +714,16 @@ struct Chunks {
     int nsplit, chunk;
 };
 
-// key chunks of the histogram passes: ~4 workgroups per CU over all groups
+// key chunks of the passes: ~4 workgroups per CU over all groups, at most
+// kMaxSplit chunks of at most kMaxChunk keys
 Chunks chunks_for(int batch, int hq, int hkv, int S) {
     const int G = pick_g(hq / hkv);
     const int groups = batch * hkv * ((hq / hkv) / G);
     const int tiles = (S + 63) / 64;
     int nsplit = (4 * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
+    if (nsplit > kMaxSplit) nsplit = kMaxSplit;
+    const int min_split = (tiles + kMaxChunk / 64 - 1) / (kMaxChunk / 64);
+    if (nsplit < min_split) nsplit = min_split;
     if (nsplit > tiles) nsplit = tiles;
     if (nsplit < 1) nsplit = 1;
     const int tiles_per = (tiles + nsplit - 1) / nsplit > 0 ? (tiles + nsplit - 1) / nsplit : 1;
@@ -484,43 +735,46 @@ Chunks chunks_for(int batch, int hq, int hkv, int S) {
 }
 
 struct Layout {
-    size_t hist, prefix, remain, cutoff, pcs, attn, total;
+    size_t hist, prefix, remain, cutoff, pcs, lists, counts, attn, total;
 };
 
 Layout layout(int batch, int hq, int hkv, int S, int d) {
     Layout L;
     const size_t bh = (size_t)batch * hq;
     const Chunks c = chunks_for(batch, hq, hkv, S);
+    const size_t regions = bh * (size_t)c.nsplit * 4;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.hist = 0;
     L.prefix = al(L.hist + bh * (size_t)c.nsplit * kBins * 4);
     L.remain = al(L.prefix + bh * 4);
     L.cutoff = al(L.remain + bh * 4);
     L.pcs = al(L.cutoff + bh * 4);
-    L.attn = al(L.pcs + bh * (size_t)bc::pcs_stride(S) * (d > 255 ? 2 : 1));
+    L.lists = al(L.pcs + bh * (size_t)bc::pcs_stride(S) * (d > 255 ? 2 : 1));
+    L.counts = al(L.lists + regions * (size_t)list_wave_cap(c.chunk) * 4);
+    L.attn = al(L.counts + regions * 4);
     L.total = L.attn + bc::attention_ws_bytes(batch, hq, hkv, S, d);
     return L;
 }
 
 template <int D, int G>
-void run_passes(const SelArgs& a, int splits_y, int chunk, int nsplit, int bh, int top_k,
-                hipStream_t st) {
-    const dim3 grid(nsplit, splits_y);
-    for (int pass = 0; pass < 3; pass++) {
-        hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a, pass, chunk);
-        hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, pass, top_k);
-    }
-    hipLaunchKernelGGL((tie_locate_kernel<D, G>), dim3(bh), dim3(256), 0, st, a);
+void run_select(const SelArgs& a, int groups, int bh, int top_k, hipStream_t st) {
+    const dim3 grid(a.nsplit, groups);
+    hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, top_k);
+    if (a.oct)
+        hipLaunchKernelGGL((collect_kernel<D, G, true>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((collect_kernel<D, G, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(final_kernel, dim3(bh), dim3(kFinalThreads), 0, st, a);
 }
 
 template <int D>
-void run_passes_g(int G, const SelArgs& a, int groups, int chunk, int nsplit, int bh, int top_k,
-                  hipStream_t st) {
+void run_select_g(int G, const SelArgs& a, int groups, int bh, int top_k, hipStream_t st) {
     switch (G) {
-        case 8: run_passes<D, 8>(a, groups, chunk, nsplit, bh, top_k, st); break;
-        case 4: run_passes<D, 4>(a, groups, chunk, nsplit, bh, top_k, st); break;
-        case 2: run_passes<D, 2>(a, groups, chunk, nsplit, bh, top_k, st); break;
-        default: run_passes<D, 1>(a, groups, chunk, nsplit, bh, top_k, st); break;
+        case 8: run_select<D, 8>(a, groups, bh, top_k, st); break;
+        case 4: run_select<D, 4>(a, groups, bh, top_k, st); break;
+        case 2: run_select<D, 2>(a, groups, bh, top_k, st); break;
+        default: run_select<D, 1>(a, groups, bh, top_k, st); break;
     }
 }
 
@@ -533,6 +787,8 @@ extern "C" int bc_adaptive_attention_workspace_size(int batch, int n_heads, int 
                    n_heads % n_kv_heads == 0,
                BC_ERR_INVALID_ARGUMENT, "invalid dims");
     BC_REQUIRE(bytes != nullptr, BC_ERR_INVALID_ARGUMENT, "null bytes");
+    BC_REQUIRE(seq_len <= kMaxSplit * kMaxChunk, BC_ERR_UNSUPPORTED,
+               "adaptive attention: seq_len %d above %d", seq_len, kMaxSplit * kMaxChunk);
     *bytes = layout(batch, n_heads, n_kv_heads, seq_len, head_dim).total;
     return BC_OK;
 }
@@ -547,6 +803,8 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
                    n_heads % n_kv_heads == 0 && kv_stride >= seq_len,
                BC_ERR_INVALID_ARGUMENT, "invalid dims");
     BC_REQUIRE(top_k >= 0, BC_ERR_INVALID_ARGUMENT, "top_k must be >= 0");
+    BC_REQUIRE(seq_len <= kMaxSplit * kMaxChunk, BC_ERR_UNSUPPORTED,
+               "adaptive attention: seq_len %d above %d", seq_len, kMaxSplit * kMaxChunk);
     if ((int64_t)batch * n_heads == 0) return BC_OK;
     BC_REQUIRE(q && k_bin && k_res && v_bin && v_res && out, BC_ERR_INVALID_ARGUMENT,
                "null pointer");
@@ -569,23 +827,25 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     a.remain = (int32_t*)(ws + L.remain);
     a.cutoff = (int32_t*)(ws + L.cutoff);
     a.pcs = ws + L.pcs;
+    a.lists = (uint32_t*)(ws + L.lists);
+    a.counts = (uint32_t*)(ws + L.counts);
     a.oct = kv_stride % 8 == 0 && ((uintptr_t)a.kb.scales % 16) == 0;
     const int G = pick_g(n_heads / n_kv_heads);
     const int groups = batch * n_kv_heads * ((n_heads / n_kv_heads) / G);
     const Chunks c = chunks_for(batch, n_heads, n_kv_heads, seq_len);
-    const int nsplit = c.nsplit, chunk = c.chunk;
-    a.nsplit = nsplit;
-    a.chunk = chunk;
+    a.nsplit = c.nsplit;
+    a.chunk = c.chunk;
+    a.wcap = list_wave_cap(c.chunk);
     const int k = top_k > seq_len ? seq_len : top_k;
     switch (head_dim) {
-        case 32: run_passes_g<32>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 64: run_passes_g<64>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 96: run_passes_g<96>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 128: run_passes_g<128>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 160: run_passes_g<160>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 192: run_passes_g<192>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 224: run_passes_g<224>(G, a, groups, chunk, nsplit, bh, k, st); break;
-        case 256: run_passes_g<256>(G, a, groups, chunk, nsplit, bh, k, st); break;
+        case 32: run_select_g<32>(G, a, groups, bh, k, st); break;
+        case 64: run_select_g<64>(G, a, groups, bh, k, st); break;
+        case 96: run_select_g<96>(G, a, groups, bh, k, st); break;
+        case 128: run_select_g<128>(G, a, groups, bh, k, st); break;
+        case 160: run_select_g<160>(G, a, groups, bh, k, st); break;
+        case 192: run_select_g<192>(G, a, groups, bh, k, st); break;
+        case 224: run_select_g<224>(G, a, groups, bh, k, st); break;
+        case 256: run_select_g<256>(G, a, groups, bh, k, st); break;
         default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
     }
     int rc = bc::check_launch("adaptive select");
