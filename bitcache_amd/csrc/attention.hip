@@ -107,6 +107,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     constexpr int R = 64 / LPK;           // key subgroups in the value phase
     constexpr int KPL = (64 + R - 1) / R; // keys per value lane per tile
     constexpr bool RES = MODE != MODE_BINARY;
+    // every key's residual data is read (compensated, and per-head modes)
+    constexpr bool ALLRES = MODE == MODE_COMP || MODE == MODE_MIXED;
 
     __shared__ QPrep<D> qp[G];
     __shared__ float qf[G * D];
@@ -159,6 +161,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             cutoff[g] = a.cutoff[bhq0 + g];
         }
     }
+    // per-head modes: which heads of the group add their residual
+    bool hm[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) hm[g] = MODE != MODE_MIXED || a.head_mode[bhq0 + g] != 0;
 
     for (int t0 = key_begin + wave * 64; t0 < key_end; t0 += 4 * 64) {
         // ---------------- issue value loads (independent of scores)
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             if (vr < R && sl < 64 && s < key_end) {
                 const int64_t vi = kv_base + s;
                 vsigns[k] = ((const uint32_t*)(a.vb.signs + vi * (D / 8)))[vc];
-                if constexpr (MODE == MODE_COMP)
+                if constexpr (ALLRES)
                     vcodes[k] = ((const uint4*)(a.vr.codes + vi * (D / 2)))[vc];
             }
         }
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         const float svv = h2f(a.vb.scales[ki]);
         float rsk = 0.0f, rsv = 0.0f;
         uint32_t kcodes[D / 8];
-        if constexpr (MODE == MODE_COMP) {
+        if constexpr (ALLRES) {
             rsk = h2f(a.kr.scales[ki]);
             rsv = h2f(a.vr.scales[ki]);
             const uint4* cp = (const uint4*)(a.kr.codes + ki * (D / 2));
@@ -239,9 +245,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float score = sc[g];
-            if constexpr (MODE == MODE_COMP) {
-                const float rdot = residual_dot_pairs<D>(kcodes, qp[g]) * (rsk / 7.0f);
-                score = score + rdot;
+            if constexpr (ALLRES) {
+                if (hm[g]) {
+                    const float rdot = residual_dot_pairs<D>(kcodes, qp[g]) * (rsk / 7.0f);
+                    score = score + rdot;
+                }
             } else if constexpr (MODE == MODE_ADAPTIVE) {
                 if ((selmask >> g) & 1u) {
                     const float rdot = residual_dot_pairs<D>(kcodes, qp[g]) * (rsk / 7.0f);
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
             const float p = valid ? exp2f(s2 - mn) : 0.0f;
             lsum[g] += p;
             float rv = 0.0f;
-            if constexpr (MODE == MODE_COMP) rv = p * (rsv / 7.0f);
+            if constexpr (ALLRES) rv = hm[g] ? p * (rsv / 7.0f) : 0.0f;
             if constexpr (MODE == MODE_ADAPTIVE) rv = ((selmask >> g) & 1u) ? p * (rsv / 7.0f) : 0.0f;
             wl[wave][g][lane] = make_float2(2.0f * p * svv, rv);
         }
@@ -423,14 +431,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* ws, uint
 // Exact attention over dense fp16 K/V [B, Hkv, S, D] with fp32 accumulation,
 // the same split / online-softmax structure and partial format as the
 // compressed kernels.  A key row (2D bytes) is read by LPR = D/8 lanes, 16
-// bytes each, so every load instruction covers whole rows (64 lanes = 1 KiB);
-// a wave takes NR such loads of K and of V per tile (TK = NR * 64/LPR keys).
+// bytes each, in a slot of LP lanes (LPR rounded up to a power of two; the
+// lanes past LPR load nothing and add zeros), so every load instruction
+// covers whole rows; a wave takes NR such loads of K and of V per tile
+// (TK = NR * 64/LP <= 64 keys).
 // q.k: 4 v_dot2_f32_f16 per lane and a sum over the row's lanes (DPP);
 // softmax with lane = key; p*v: 8 mixed-precision FMAs per lane, reduced over
 // the rows of the tile once at the end.
 template <int LPR>
 __device__ __forceinline__ float row_sum_f(float v) {
-    if constexpr (LPR == 8) {
+    if constexpr (LPR == 4) {
+        v += dpp_f<0x4E>(v);
+        v += dpp_f<0xB1>(v);
+    } else if constexpr (LPR == 8) {
         v += dpp_f<0x141>(v);   // half mirror
         v += dpp_f<0x4E>(v);
         v += dpp_f<0xB1>(v);
@@ -448,10 +461,11 @@ template <int D, int G>
 __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const uint16_t* K,
                                                        const uint16_t* V, int Hq, int Hkv, int S,
                                                        int n_splits, int chunk, float* ws) {
-    constexpr int LPR = D / 8;           // lanes per key row
-    constexpr int RPI = 64 / LPR;        // rows per load instruction
-    constexpr int NR = 8;                // loads of K (and of V) per tile
-    constexpr int TK = NR * RPI;         // keys per tile
+    constexpr int LPR = D / 8;           // lanes holding a key row
+    constexpr int LP = LPR <= 4 ? 4 : (LPR <= 8 ? 8 : (LPR <= 16 ? 16 : 32));   // lane slot per row
+    constexpr int RPI = 64 / LP;         // rows per load instruction
+    constexpr int NR = 8 * RPI <= 64 ? 8 : 64 / RPI;   // loads of K (and of V) per tile
+    constexpr int TK = NR * RPI;         // keys per tile (at most 64: lane = key below)
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     __shared__ float sc[4][G][64];
     __shared__ float red[4][RPI][D];
@@ -466,7 +480,8 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
     const int hq0 = kvh * (Hq / Hkv) + qg * G;
     const int bhq0 = b * Hq + hq0;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int row = lane / LPR, part = lane % LPR;
+    const int row = lane / LP, part = lane % LP;
+    const bool act = part < LPR;         // (a lane past the row's 16-byte pieces)
     const int key_begin = split * chunk, key_end = min(S, key_begin + chunk);
     const int64_t base = (int64_t)bkv * S;
     const float isd2 = (1.0f / sqrtf((float)D)) * kLog2e;
@@ -474,7 +489,7 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
     h2 qp[G][4];   // this lane's 8 query dims (part*8 ..) per head
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        const uint4 w = ((const uint4*)(q + (int64_t)(bhq0 + g) * D))[part];
+        const uint4 w = act ? ((const uint4*)(q + (int64_t)(bhq0 + g) * D))[part] : make_uint4(0, 0, 0, 0);
         qp[g][0] = __builtin_bit_cast(h2, w.x);
         qp[g][1] = __builtin_bit_cast(h2, w.y);
         qp[g][2] = __builtin_bit_cast(h2, w.z);
@@ -495,8 +510,9 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
             const int key = t0 + i * RPI + row;
             const int64_t ki = base + (key < key_end ? key : t0);
             // nontemporal: each instruction reads whole rows once
-            const bc_v4u kv = __builtin_nontemporal_load((const bc_v4u*)(K + ki * D) + part);
-            const bc_v4u vv = __builtin_nontemporal_load((const bc_v4u*)(V + ki * D) + part);
+            const bc_v4u z = {0u, 0u, 0u, 0u};
+            const bc_v4u kv = act ? __builtin_nontemporal_load((const bc_v4u*)(K + ki * D) + part) : z;
+            const bc_v4u vv = act ? __builtin_nontemporal_load((const bc_v4u*)(V + ki * D) + part) : z;
             kr[i] = make_uint4(kv[0], kv[1], kv[2], kv[3]);
             vr[i] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
         }
@@ -511,7 +527,7 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
                 d = __builtin_amdgcn_fdot2(qp[g][1], __builtin_bit_cast(h2, kr[i].y), d, false);
                 d = __builtin_amdgcn_fdot2(qp[g][2], __builtin_bit_cast(h2, kr[i].z), d, false);
                 d = __builtin_amdgcn_fdot2(qp[g][3], __builtin_bit_cast(h2, kr[i].w), d, false);
-                d = row_sum_f<LPR>(d);
+                d = row_sum_f<LP>(d);
                 if (part == 0) sc[wave][g][i * RPI + row] = valid ? d * isd2 : -INFINITY;
             }
         }
@@ -564,7 +580,8 @@ __global__ __launch_bounds__(256) void ref_split_kernel(const uint16_t* q, const
             wlsum[wave][g] = l_w;
         }
 #pragma unroll
-        for (int e = 0; e < 8; e++) red[wave][row][part * 8 + e] = acc[g][e];
+        for (int e = 0; e < 8; e++)
+            if (act) red[wave][row][part * 8 + e] = acc[g][e];
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -890,6 +907,8 @@ void launch_split(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_BINARY>), grid, dim3(256), 0, st, a);
     else if (mode == MODE_COMP)
         hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_COMP>), grid, dim3(256), 0, st, a);
+    else if (mode == MODE_MIXED)
+        hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_MIXED>), grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((attn_split_kernel<D, G, MODE_ADAPTIVE>), grid, dim3(256), 0, st, a);
 }
@@ -984,8 +1003,6 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.out = nullptr;
     // (the VALU kernel does not append; the append entry point checks first)
     BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
-    BC_REQUIRE(mode != MODE_MIXED, BC_ERR_UNSUPPORTED,
-               "per-head modes need the MFMA kernel (head_dim 64, 128 or 256)");
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }
@@ -1188,8 +1205,6 @@ extern "C" int bc_head_mode_attention(const void* q, const void* k_bin, const vo
                                       void* out, int batch, int n_heads, int n_kv_heads, int seq_len,
                                       int kv_stride, int head_dim, void* workspace,
                                       size_t workspace_bytes, void* stream) {
-    BC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, BC_ERR_UNSUPPORTED,
-               "per-head modes: head_dim 64, 128 or 256, got %d", head_dim);
     BC_REQUIRE(k_res && v_res, BC_ERR_INVALID_ARGUMENT, "residual blobs required");
     BC_REQUIRE(modes != nullptr || (int64_t)batch * n_heads == 0, BC_ERR_INVALID_ARGUMENT,
                "null modes");
@@ -1283,8 +1298,6 @@ extern "C" int bc_reference_attention(const void* q, const void* k, const void* 
                                       void* stream) {
     int vv = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
     if (vv != BC_OK) return vv;
-    BC_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, BC_ERR_UNSUPPORTED,
-               "reference attention supports head_dim 64, 128 or 256, got %d", head_dim);
     if ((int64_t)batch * n_heads == 0) return BC_OK;
     BC_REQUIRE(q && k && v && out, BC_ERR_INVALID_ARGUMENT, "null pointer");
     const size_t need_ws = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
@@ -1293,12 +1306,8 @@ extern "C" int bc_reference_attention(const void* q, const void* k, const void* 
     const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, kPlanFixed);
     const dim3 grid(p.n_splits, batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G));
     hipStream_t st = (hipStream_t)stream;
-    switch (head_dim) {
-        case 64: launch_ref<64>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
-        case 128: launch_ref<128>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
-        case 256: launch_ref<256>(p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits, p.chunk, (float*)workspace, grid, st); break;
-        default: return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
-    }
+    BC_DISPATCH_D(head_dim, launch_ref, p.G, q, k, v, n_heads, n_kv_heads, seq_len, p.n_splits,
+                  p.chunk, (float*)workspace, grid, st);
     int rc = bc::check_launch("reference attention");
     if (rc != BC_OK) return rc;
     BC_DISPATCH_D(head_dim, launch_combine, (const float*)workspace, (uint16_t*)out,

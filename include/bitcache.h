@@ -193,7 +193,8 @@ int bc_attention_combine(const void* workspace, void* out, int batch, int n_head
  * bc_adaptive_select from bc_compute_head_entropy).  The reference's intent
  * for adaptive precision (src/adaptive_precision.cuh:6-49), which its demo
  * dispatches per layer in Python (examples/generation_demo.py:129-141).
- * head_dim 64, 128 or 256; workspace as bc_attention_workspace_size. */
+ * head_dim a multiple of 32 up to 256 (the matrix-core kernel at 64, 128 and
+ * 256, the VALU kernel otherwise); workspace as bc_attention_workspace_size. */
 int bc_head_mode_attention(const void* q, const void* k_bin, const void* k_res, const void* v_bin,
                            const void* v_res, const uint8_t* modes, void* out, int batch,
                            int n_heads, int n_kv_heads, int seq_len, int kv_stride, int head_dim,

@@ -131,11 +131,11 @@ def test_attention_argument_errors(lib, no_gpu):
     assert f(*[fake] * 8, 1, 4, 4, 128, 5, 16, fake, 1, None) == BC_ERR_WORKSPACE   # before the token is written
     r = lib.bc_reference_attention
     r.argtypes = [P] * 4 + [ctypes.c_int] * 5 + [P, size_t, P]
-    assert r(fake, fake, fake, fake, 1, 4, 4, 100, 96, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
+    assert r(fake, fake, fake, fake, 1, 4, 4, 100, 100, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
     h = lib.bc_head_mode_attention
     h.argtypes = [P] * 7 + [ctypes.c_int] * 6 + [P, size_t, P]
     modes = P(0x2000)
-    assert h(*[fake] * 5, modes, fake, 1, 4, 4, 100, 100, 96, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
+    assert h(*[fake] * 5, modes, fake, 1, 4, 4, 100, 100, 100, fake, 1 << 30, None) == BC_ERR_UNSUPPORTED
     assert h(*[fake] * 5, None, fake, 1, 4, 4, 100, 100, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
     assert h(fake, fake, None, fake, fake, modes, fake, 1, 4, 4, 100, 100, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
     assert h(*[fake] * 5, modes, fake, 1, 4, 4, 100, 100, 128, fake, 1, None) == BC_ERR_WORKSPACE

@@ -230,7 +230,10 @@ def test_entropy_vs_oracle(F):
     assert np.array_equal(modes, (ent < np.median(ent)).astype(np.uint8))
 
 
-@pytest.mark.parametrize("shape", [(1, 4, 4, 1000, 128), (2, 8, 2, 777, 64), (1, 2, 2, 64, 256)])
+@pytest.mark.parametrize("shape", [(1, 4, 4, 1000, 128), (2, 8, 2, 777, 64), (1, 2, 2, 64, 256),
+                                   # head dims whose rows do not fill a power-of-two lane slot
+                                   (1, 4, 2, 500, 32), (1, 4, 4, 333, 96), (1, 2, 2, 300, 160),
+                                   (1, 4, 2, 257, 192), (1, 8, 2, 200, 224)])
 def test_reference_attention_vs_oracle(F, shape):
     B, Hq, Hkv, S, d = shape
     say(f"case reference_attention {shape}")
@@ -387,7 +390,10 @@ def test_gqa_equals_mha_on_repeated_kv(F, group, d):
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,d", [(2, 8, 8, 1500, 128), (2, 16, 4, 2000, 128),
-                                          (1, 8, 2, 900, 64), (1, 4, 4, 700, 256)])
+                                          (1, 8, 2, 900, 64), (1, 4, 4, 700, 256),
+                                          # the VALU kernel's per-head modes
+                                          (1, 4, 4, 500, 32), (1, 8, 2, 600, 96),
+                                          (1, 4, 2, 300, 160), (1, 8, 4, 250, 224)])
 def test_head_mode_attention(F, B, Hq, Hkv, S, d):
     """Per-head dispatch in one launch: heads with mode 0 match the oracle's
     binary attention, heads with mode 1 its compensated attention (modes mixed

@@ -11,7 +11,7 @@ most delta/2 = max|q| / 61166, the same absolute bound on every element, so
 elements far below max|q| keep fewer significant bits; these cases bound what
 that costs on the outputs: compensated MHA and GQA, adaptive top-k (whose
 selection uses only the exact binary key) and per-head modes, at d = 64, 128
-and 256, plus the VALU kernel's head dims."""
+and 256, plus the VALU kernel's head dims (fp32 residual dot)."""
 import numpy as np
 import pytest
 import torch
@@ -102,13 +102,13 @@ def test_compensated_and_adaptive_with_extreme_queries(shape, kind):
     for (b, h), idx in sets.items():
         assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"set differs at ({b}, {h})"
     close(to_np(aout).astype(np.float32), aref, what=f"adaptive {kind} {shape}")
-    if d in (64, 128, 256):
-        modes = torch.from_numpy((np.arange(B * Hq) % 2).astype(np.uint8).reshape(B, Hq)).cuda()
-        mout = F.head_mode_attention(qt, kb, kr, vb, vr, modes, B, Hq, S, d, n_kv_heads=Hkv)
-        _, bref = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
-        got = to_np(mout).astype(np.float32)
-        m = to_np(modes)
-        for b in range(B):
-            for h in range(Hq):
-                close(got[b, h], ref[b, h] if m[b, h] else bref[b, h],
-                      what=f"head mode {kind} {shape} ({b},{h})")
+    # per-head modes (the matrix-core kernel at 64/128/256, the VALU one otherwise)
+    modes = torch.from_numpy((np.arange(B * Hq) % 2).astype(np.uint8).reshape(B, Hq)).cuda()
+    mout = F.head_mode_attention(qt, kb, kr, vb, vr, modes, B, Hq, S, d, n_kv_heads=Hkv)
+    _, bref = O.binary_attention(q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
+    got = to_np(mout).astype(np.float32)
+    m = to_np(modes)
+    for b in range(B):
+        for h in range(Hq):
+            close(got[b, h], ref[b, h] if m[b, h] else bref[b, h],
+                  what=f"head mode {kind} {shape} ({b},{h})")
