@@ -6,32 +6,32 @@
 //   1. hist_kernel: the popcounts of every key from the K sign planes, stored
 //      (one byte per query head and key, two for d = 256: the later launches
 //      and the attention pass read them instead of the d/8-byte sign rows),
-//      and per key chunk a histogram of the keys' top 11 bits;
+//      and per key chunk a histogram of the keys' top 13 bits (16-bit counts);
 //   2. pick_kernel: per (b, head), sums the chunk histograms and picks the
-//      bucket (top-11-bit digit) holding the k-th largest key; `remain` keys
+//      bucket (top-13-bit digit) holding the k-th largest key; `remain` keys
 //      are still to be taken from it;
-//   3. collect_kernel: lists the keys of that bucket (about 4% of a head's
+//   3. collect_kernel: lists the keys of that bucket (about 1% of a head's
 //      keys at k = S/10 on Gaussian data), each as one 32-bit entry holding
-//      key bits 20..6 and the index in its chunk;
+//      key bits 18..6 and the index in its chunk;
 //   4. final_kernel: per (b, head), an exact radix select of the remain-th
 //      largest listed key (T; `need` keys equal to T are taken), then the
 //      need-th smallest index among the listed keys equal to T (ties are
 //      taken lowest index first) as the cutoff.
 // The attention kernel selects key > T, or key == T at an index <= cutoff.
 //
-// Why key bits 20..6 identify a listed key: with a finite fp16 scale the
+// Why key bits 18..6 identify a listed key: with a finite fp16 scale the
 // score is an exact fp32 product of an 11-bit significand and an even integer
 // of magnitude <= 256 (at most 18 significant bits), so its low 6 bits are
 // zero, as are those of +-inf and +0.  The ordered key therefore ends in six
 // 0 bits when bit 31 is set (scores >= +0) and in six 1 bits otherwise (the
 // key of a negative score is the complement; NaN ranks as -inf).  Listed keys
-// share bits 31..21 (the bucket), which fixes the rest.
+// share bits 31..19 (the bucket), which fixes the rest.
 //
 // Scores are compared as exact floats against bounds derived from the key
 // prefix (see key_floor), which order like the keys; a wave holding a
 // non-finite scale compares the keys themselves.
 //
-// Workspace: chunk histograms [B*Hq][nsplit][2048] u32 | prefix [B*Hq] u32
+// Workspace: chunk histograms [B*Hq][hsplit][8192] u16 | prefix [B*Hq] u32
 //   | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G]
 //   | bucket lists [B*Hq][nsplit][4 waves][wcap] u32 | list counts [B*Hq][nsplit][4] u32
 //   | attention partials.
@@ -41,7 +41,14 @@ namespace {
 using bc::PcPack;
 using bc::PcT;
 
-constexpr int kBins = 2048;
+constexpr int kBins = 2048;             // radix rounds of the final select
+constexpr int kTopBits = 13;            // the first digit (bucket): key bits 31..19
+constexpr int kTopShift = 32 - kTopBits;
+constexpr int kTopBins = 1 << kTopBits; // counted as 16-bit halves of 32-bit words
+constexpr uint32_t kTopMask = ~0u << kTopShift;
+constexpr int kLowBits = kTopShift - 6; // listed key bits 18..6
+constexpr int kHistThreads = 512;
+constexpr int kMaxHistTiles = 1023;     // 64-key tiles per histogram chunk (counts < 2^16)
 constexpr int kMaxSplit = 1024;       // key chunks per head
 constexpr int kMaxChunk = 65536;      // keys per chunk (16-bit indices in the lists)
 constexpr int kFinalThreads = 512;
@@ -53,10 +60,12 @@ struct SelArgs {
     const uint16_t* q;
     BinPlanes kb;
     int Hq, Hkv, S, kv_stride;
-    int nsplit, chunk;   // key chunks of the passes (chunk: a multiple of 64, <= kMaxChunk)
+    int hsplit, hchunk;  // key chunks of the histogram pass (hchunk <= 64 * kMaxHistTiles)
+    int nsplit, chunk;   // key chunks of the collect pass (chunk: a multiple of 64, <= kMaxChunk)
     int wcap;            // list entries per (head, chunk, wave)
-    uint32_t* hist;      // [B*Hq][nsplit][2048] each key chunk's top-digit histogram
-    uint32_t* prefix;    // [B*Hq] bucket digit << 21, then the threshold T
+    uint32_t* hist;      // [B*Hq][hsplit][kTopBins / 2] each key chunk's top-digit histogram
+                         // (bin b: half b & 1 of word b >> 1)
+    uint32_t* prefix;    // [B*Hq] bucket digit << kTopShift, then the threshold T
     int32_t* remain;     // [B*Hq] keys still to take from the bucket, then at T
     int32_t* cutoff;     // [B*Hq]
     void* pcs;           // [B*Hq/G][pcs_stride(S)][G] popcounts (PcT<D>)
@@ -90,40 +99,45 @@ __device__ __forceinline__ uint32_t key_of_pc(int pc, float sk) {
 }
 
 // Every key of a chunk: the popcounts of the G heads of the group (stored)
-// and each head's histogram of the top 11 key bits, stored whole for the
-// chunk (plain coalesced stores; the pick sums the chunks).
-// grid: (nsplit, B*Hkv*(group/G)); block 256.
+// and each head's histogram of the top 13 key bits, 16-bit counts two to a
+// word (a chunk holds fewer than 2^16 keys), stored whole for the chunk
+// (plain coalesced stores; the pick sums the chunks).
+// grid: (hsplit, B*Hkv*(group/G)); block kHistThreads.
 template <int D, int G>
-__global__ __launch_bounds__(256) void hist_kernel(SelArgs a) {
+__global__ __launch_bounds__(kHistThreads) void hist_kernel(SelArgs a) {
     __shared__ uint32_t qs[G][D / 32];
-    __shared__ uint32_t h[G][kBins];
+    __shared__ uint32_t h[G][kTopBins / 2];
     const int nqg = (a.Hq / a.Hkv) / G;
     const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
     const int bhq0 = b * a.Hq + kvh * (a.Hq / a.Hkv) + qg * G;
     load_q_signs<D, G>(a.q + (int64_t)bhq0 * D, qs);
-    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) (&h[0][0])[i] = 0u;
+    for (int i = threadIdx.x; i < G * kTopBins / 2; i += blockDim.x) (&h[0][0])[i] = 0u;
     __syncthreads();
     const int64_t base = (int64_t)bkv * a.kv_stride;
-    const int k0 = blockIdx.x * a.chunk, k1 = min(a.S, k0 + a.chunk);
+    const int k0 = blockIdx.x * a.hchunk, k1 = min(a.S, k0 + a.hchunk);
     using P = PcT<D>;
     using Pack = PcPack<P, G>;
     Pack* pcs = (Pack*)a.pcs + (int64_t)bhq0 / G * bc::pcs_stride(a.S);   // this group's packs
+    auto bump = [&](int g, uint32_t key) {
+        const uint32_t bin = key >> kTopShift;
+        atomicAdd(&h[g][bin >> 1], 1u << ((bin & 1u) << 4));
+    };
     auto count = [&](const Pack& pk, float sk) {
         // (a wave with a non-finite scale takes the key path for all its lanes)
         if (__ballot(!finite_scale(sk)) == 0ull) {
             const float sk2 = 2.0f * sk, nd = -(float)D * sk;
 #pragma unroll
-            for (int g = 0; g < G; g++) atomicAdd(&h[g][ordered_bits(fmaf((float)pk.v[g], sk2, nd)) >> 21], 1u);
+            for (int g = 0; g < G; g++) bump(g, ordered_bits(fmaf((float)pk.v[g], sk2, nd)));
         } else {
 #pragma unroll
-            for (int g = 0; g < G; g++) atomicAdd(&h[g][key_of_pc<D>((int)pk.v[g], sk) >> 21], 1u);
+            for (int g = 0; g < G; g++) bump(g, key_of_pc<D>((int)pk.v[g], sk));
         }
     };
     // Two register stages of UP keys per thread: the loads of the next stage
     // are in flight while a stage is counted.
     constexpr int UP = D >= 256 ? 2 : 4;
-    constexpr int step = UP * 256;
+    constexpr int step = UP * kHistThreads;
     struct Stage {
         SignWords<D> ks[UP];
         uint16_t sk[UP];
@@ -131,7 +145,7 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a) {
     auto load = [&](Stage& st, int s) {
 #pragma unroll
         for (int u = 0; u < UP; u++) {
-            const int ss = s + u * 256;
+            const int ss = s + u * kHistThreads;
             const int64_t i = base + (ss < k1 ? ss : k0);
             st.ks[u] = load_signs<D, true>(a.kb.signs + i * (D / 8));
             st.sk[u] = a.kb.scales[i];
@@ -140,7 +154,7 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a) {
     auto run = [&](const Stage& st, int s) {
 #pragma unroll
         for (int u = 0; u < UP; u++) {
-            const int ss = s + u * 256;
+            const int ss = s + u * kHistThreads;
             if (ss >= k1) break;
             Pack pk;
 #pragma unroll
@@ -165,41 +179,44 @@ __global__ __launch_bounds__(256) void hist_kernel(SelArgs a) {
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * kBins; i += blockDim.x) {
-        const int g = i / kBins, bin = i % kBins;
-        a.hist[((int64_t)(bhq0 + g) * a.nsplit + blockIdx.x) * kBins + bin] = h[g][bin];
+    for (int i = threadIdx.x; i < G * kTopBins / 2; i += blockDim.x) {
+        const int g = i / (kTopBins / 2), w = i % (kTopBins / 2);
+        a.hist[((int64_t)(bhq0 + g) * a.hsplit + blockIdx.x) * (kTopBins / 2) + w] = h[g][w];
     }
 }
 
 // One block per (b, query head): sum the chunk histograms and pick the bucket
-// (top-11-bit digit) holding the top_k-th largest key: prefix = digit << 21,
-// remain = top_k - (keys above the bucket).
+// (top-13-bit digit) holding the top_k-th largest key:
+// prefix = digit << kTopShift, remain = top_k - (keys above the bucket).
+// Thread t sums bins [kTopBins - 32 (t + 1), kTopBins - 32 t) of every chunk
+// in registers, so the threads in order hold descending bin groups.
 __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int top_k) {
-    __shared__ uint32_t cnt[kBins];
+    constexpr int kPer = kTopBins / 256;   // bins per thread
     __shared__ uint32_t part[256];
     const int bhq = blockIdx.x;
-    const uint32_t* h = a.hist + (int64_t)bhq * a.nsplit * kBins;
-    {
-        // eight consecutive bins per thread
-        const int b0 = threadIdx.x * 8;
-        uint32_t sum[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-        for (int c = 0; c < a.nsplit; c++) {
-            const bc_v4u x = *(const bc_v4u*)(h + (int64_t)c * kBins + b0);
-            const bc_v4u y = *(const bc_v4u*)(h + (int64_t)c * kBins + b0 + 4);
-            sum[0] += x[0]; sum[1] += x[1]; sum[2] += x[2]; sum[3] += x[3];
-            sum[4] += y[0]; sum[5] += y[1]; sum[6] += y[2]; sum[7] += y[3];
-        }
+    const uint32_t* h = a.hist + (int64_t)bhq * a.hsplit * (kTopBins / 2);
+    const int b0 = kTopBins - kPer * ((int)threadIdx.x + 1);
+    uint32_t cnt[kPer];
 #pragma unroll
-        for (int j = 0; j < 8; j++) cnt[b0 + j] = sum[j];
+    for (int j = 0; j < kPer; j++) cnt[j] = 0u;
+    for (int c = 0; c < a.hsplit; c++) {
+        const bc_v4u* src = (const bc_v4u*)(h + (int64_t)c * (kTopBins / 2) + b0 / 2);
+#pragma unroll
+        for (int v = 0; v < kPer / 8; v++) {
+            const bc_v4u x = src[v];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                cnt[8 * v + 2 * e] += x[e] & 0xFFFFu;
+                cnt[8 * v + 2 * e + 1] += x[e] >> 16;
+            }
+        }
     }
-    __syncthreads();
-    const int remain = top_k;
-    // per-thread counts of 8 consecutive bins (descending digits)
-    constexpr int per = kBins / 256;
     uint32_t local = 0;
-    for (int j = 0; j < per; j++) local += cnt[kBins - 1 - (threadIdx.x * per + j)];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) local += cnt[j];
     part[threadIdx.x] = local;
     __syncthreads();
+    const int remain = top_k;
     if (remain <= 0) {
         if (threadIdx.x == 0) {
             a.prefix[bhq] = 0xFFFFFFFFu;  // nothing selected: no key exceeds it, no tie taken
@@ -223,18 +240,22 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int top_k) {
         a.remain[bhq] = 0;
     }
     if (excl < (uint32_t)remain && incl >= (uint32_t)remain) {
-        // this thread's 8 bins hold the remain-th largest key
+        // this thread's bins hold the remain-th largest key: from its top bin down
         uint32_t above = excl;
-        int digit = 0;
-        for (int j = 0; j < per; j++) {
-            const int d = kBins - 1 - (threadIdx.x * per + j);
-            if (above + cnt[d] >= (uint32_t)remain) {
-                digit = d;
-                break;
+        int digit = b0;
+        bool found = false;
+#pragma unroll
+        for (int j = kPer - 1; j >= 0; j--) {
+            if (!found) {
+                if (above + cnt[j] >= (uint32_t)remain) {
+                    digit = b0 + j;
+                    found = true;
+                } else {
+                    above += cnt[j];
+                }
             }
-            above += cnt[d];
         }
-        a.prefix[bhq] = (uint32_t)digit << 21;
+        a.prefix[bhq] = (uint32_t)digit << kTopShift;
         a.remain[bhq] = remain - (int)above;
     }
 }
@@ -255,9 +276,9 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The bucket lists: every key of the chunk whose top 11 bits are the picked
+// The bucket lists: every key of the chunk whose top 13 bits are the picked
 // bucket of a head goes into that head's list as
-// (key bits 20..6) << 16 | (index - chunk start).  A wave gathers the entries
+// (key bits 18..6) << 16 | (index - chunk start).  A wave gathers the entries
 // of a row of 512 keys in its LDS area (ballot counts, no atomics), then
 // appends them to its own list region with whole-wave stores, so a row costs
 // one store per head instead of one per key step and head; it stores its
@@ -293,8 +314,8 @@ __global__ __launch_bounds__(256) void collect_kernel(SelArgs a) {
     for (int g = 0; g < G; g++) {
         const int bhq = bhq0 + g;
         live[g] = a.remain[bhq] > 0;
-        klo[g] = a.prefix[bhq] & 0xFFE00000u;
-        khi[g] = klo[g] | 0x001FFFFFu;
+        klo[g] = a.prefix[bhq] & kTopMask;
+        khi[g] = klo[g] | ~kTopMask;
         flo[g] = klo[g] == 0u ? -INFINITY : key_floor(klo[g] - 1u);
         fhi[g] = key_floor(khi[g]);
         lst[g] = a.lists + (((int64_t)bhq * a.nsplit + blockIdx.x) * 4 + wave) * a.wcap;
@@ -327,7 +348,7 @@ __global__ __launch_bounds__(256) void collect_kernel(SelArgs a) {
                 if (mt[g]) {
                     const uint32_t below =
                         __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-                    stg[wave][g][rc[g] + below] = (((key[g] >> 6) & 0x7FFFu) << 16) | (uint32_t)(s - k0);
+                    stg[wave][g][rc[g] + below] = (((key[g] >> 6) & ((1u << kLowBits) - 1u)) << 16) | (uint32_t)(s - k0);
                 }
                 rc[g] += (uint32_t)__builtin_popcountll(m);
             }
@@ -506,7 +527,7 @@ __device__ void block_pick(const uint32_t* cnt, int nb, uint32_t r, uint32_t* ws
 // once, else every round re-reads it.
 __global__ __launch_bounds__(kFinalThreads) void final_kernel(SelArgs a) {
     constexpr int NT = kFinalThreads;
-    __shared__ uint32_t s_k[kStageCap];        // key bits 20..6
+    __shared__ uint32_t s_k[kStageCap];        // key bits 18..6
     __shared__ uint32_t s_i[kStageCap];        // key index
     __shared__ uint32_t cnt[kBins];
     __shared__ uint32_t rpre[4 * kMaxSplit + 1];
@@ -547,7 +568,7 @@ __global__ __launch_bounds__(kFinalThreads) void final_kernel(SelArgs a) {
     }
     const uint32_t n = rpre[nreg];
     // entry i of the flat list: its region is the last r with rpre[r] <= i;
-    // returns (key bits 20..6) and the key index
+    // returns (key bits 18..6) and the key index
     auto fetch = [&](uint32_t i, uint32_t& k15, uint32_t& idx) {
         int lo = 0, hi = nreg - 1;
         while (lo < hi) {
@@ -605,7 +626,7 @@ __global__ __launch_bounds__(kFinalThreads) void final_kernel(SelArgs a) {
         }
         __syncthreads();
     }
-    // fn(key bits 20..6, index) for every entry of the bucket
+    // fn(key bits 18..6, index) for every entry of the bucket
     auto each = [&](auto&& fn) {
         if (staged) {
             for (uint32_t i = threadIdx.x; i < n; i += NT) fn(s_k[i], s_i[i]);
@@ -657,8 +678,8 @@ __global__ __launch_bounds__(kFinalThreads) void final_kernel(SelArgs a) {
     };
     uint32_t r = (uint32_t)r0, t = 0;
     const uint32_t kT = select(
-        r, 15, [](uint32_t k, uint32_t) { return k; }, [](uint32_t, uint32_t) { return true; }, t);
-    const uint32_t T = (P0 & 0xFFE00000u) | (kT << 6) | ((P0 & 0x80000000u) ? 0u : 0x3Fu);
+        r, kLowBits, [](uint32_t k, uint32_t) { return k; }, [](uint32_t, uint32_t) { return true; }, t);
+    const uint32_t T = (P0 & kTopMask) | (kT << 6) | ((P0 & 0x80000000u) ? 0u : 0x3Fu);
     const uint32_t need = r;   // 1 <= need <= t
     int cutoff;
     if (need >= t) {
@@ -711,26 +732,32 @@ int pick_g(int group) {
 }
 
 struct Chunks {
-    int nsplit, chunk;
+    int nsplit, chunk;     // collect pass
+    int hsplit, hchunk;    // histogram pass
 };
 
-// key chunks of the passes: ~4 workgroups per CU over all groups, at most
-// kMaxSplit chunks of at most kMaxChunk keys
+// key chunks of the collect pass: ~4 workgroups per CU over all groups, at
+// most kMaxSplit chunks of at most kMaxChunk keys; of the histogram pass:
+// ~2 workgroups (of kHistThreads) per CU, at most kMaxHistTiles tiles each
 Chunks chunks_for(int batch, int hq, int hkv, int S) {
     const int G = pick_g(hq / hkv);
     const int groups = batch * hkv * ((hq / hkv) / G);
     const int tiles = (S + 63) / 64;
-    int nsplit = (4 * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
-    if (nsplit > kMaxSplit) nsplit = kMaxSplit;
-    const int min_split = (tiles + kMaxChunk / 64 - 1) / (kMaxChunk / 64);
-    if (nsplit < min_split) nsplit = min_split;
-    if (nsplit > tiles) nsplit = tiles;
-    if (nsplit < 1) nsplit = 1;
-    const int tiles_per = (tiles + nsplit - 1) / nsplit > 0 ? (tiles + nsplit - 1) / nsplit : 1;
+    auto split = [&](int per_cu, int most, int max_tiles, int& n, int& chunk) {
+        int ns = (per_cu * bc::device_cu_count() + groups - 1) / (groups > 0 ? groups : 1);
+        if (ns > most) ns = most;
+        const int min_split = (tiles + max_tiles - 1) / max_tiles;
+        if (ns < min_split) ns = min_split;
+        if (ns > tiles) ns = tiles;
+        if (ns < 1) ns = 1;
+        const int tiles_per = (tiles + ns - 1) / ns > 0 ? (tiles + ns - 1) / ns : 1;
+        chunk = tiles_per * 64;
+        n = (tiles + tiles_per - 1) / tiles_per;
+        if (n < 1) n = 1;
+    };
     Chunks c;
-    c.chunk = tiles_per * 64;
-    c.nsplit = (tiles + tiles_per - 1) / tiles_per;
-    if (c.nsplit < 1) c.nsplit = 1;
+    split(4, kMaxSplit, kMaxChunk / 64, c.nsplit, c.chunk);
+    split(2, 1 << 30, kMaxHistTiles, c.hsplit, c.hchunk);
     return c;
 }
 
@@ -745,7 +772,7 @@ Layout layout(int batch, int hq, int hkv, int S, int d) {
     const size_t regions = bh * (size_t)c.nsplit * 4;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.hist = 0;
-    L.prefix = al(L.hist + bh * (size_t)c.nsplit * kBins * 4);
+    L.prefix = al(L.hist + bh * (size_t)c.hsplit * (kTopBins / 2) * 4);
     L.remain = al(L.prefix + bh * 4);
     L.cutoff = al(L.remain + bh * 4);
     L.pcs = al(L.cutoff + bh * 4);
@@ -759,7 +786,7 @@ Layout layout(int batch, int hq, int hkv, int S, int d) {
 template <int D, int G>
 void run_select(const SelArgs& a, int groups, int bh, int top_k, hipStream_t st) {
     const dim3 grid(a.nsplit, groups);
-    hipLaunchKernelGGL((hist_kernel<D, G>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((hist_kernel<D, G>), dim3(a.hsplit, groups), dim3(kHistThreads), 0, st, a);
     hipLaunchKernelGGL(pick_kernel, dim3(bh), dim3(256), 0, st, a, top_k);
     if (a.oct)
         hipLaunchKernelGGL((collect_kernel<D, G, true>), grid, dim3(256), 0, st, a);
@@ -835,6 +862,8 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     const Chunks c = chunks_for(batch, n_heads, n_kv_heads, seq_len);
     a.nsplit = c.nsplit;
     a.chunk = c.chunk;
+    a.hsplit = c.hsplit;
+    a.hchunk = c.hchunk;
     a.wcap = list_wave_cap(c.chunk);
     const int k = top_k > seq_len ? seq_len : top_k;
     switch (head_dim) {
