@@ -248,6 +248,9 @@ int bc_adaptive_select(const float* entropy, uint8_t* modes, int batch, int n_he
  * key scale_k*(2*popcount-d) (ties: lowest index) use the compensated score
  * and V; the others use binary score and V; one softmax over all keys.
  * selected (optional, uint8 [batch, n_heads, seq_len]) receives the 0/1 set.
+ * seq_len up to 2^26 (BC_ERR_UNSUPPORTED above).  The workspace holds about
+ * 5 bytes per query head and key (selection lists and popcounts) plus the
+ * attention partials.
  * No counterpart in the reference (its intent: src/adaptive_precision.cuh:6-12). */
 int bc_adaptive_attention_workspace_size(int batch, int n_heads, int n_kv_heads, int seq_len,
                                          int head_dim, size_t* bytes);

@@ -112,6 +112,10 @@ def test_attention_argument_errors(lib, no_gpu):
     assert ws(8, 32, 32, 65536, 128, ctypes.byref(n)) == BC_OK and n.value > 0
     assert ws(1, 6, 4, 10, 128, ctypes.byref(n)) == BC_ERR_INVALID_ARGUMENT   # 6 % 4 != 0
     assert ws(1, 4, 4, 10, 100, ctypes.byref(n)) == BC_ERR_UNSUPPORTED
+    aws = lib.bc_adaptive_attention_workspace_size
+    aws.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(size_t)]
+    # the selection lists index keys within chunks of 2^16, at most 2^10 chunks
+    assert aws(1, 4, 4, (1 << 26) + 1, 128, ctypes.byref(n)) == BC_ERR_UNSUPPORTED
     g = lib.bc_attention_gqa
     g.argtypes = [P] * 6 + [ctypes.c_int] * 6 + [P, size_t, P]
     # workspace too small is rejected before any launch
