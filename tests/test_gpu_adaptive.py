@@ -107,8 +107,10 @@ def test_adaptive_limits(F):
 @pytest.mark.parametrize("S,k", [(10000, 1000), (3000, 300)])
 def test_adaptive_all_keys_tied(F, S, k):
     """Every key of a head equal: one score, so the k keys of lowest index are
-    taken (the three radix passes end on that score with k ties still to take,
-    and the tie scan places the cutoff index)."""
+    taken.  The whole head is one bucket (more keys than the final select
+    holds in LDS at S = 10000, so it re-reads the bucket lists each round) and
+    more than 512 keys tie, so the cutoff comes from a radix select on the
+    index."""
     say(f"case adaptive all tied S={S}")
     B, Hq, Hkv, d = 1, 4, 2, 128
     q, kx, vx = make(B, Hq, Hkv, S, d, seed=21)
@@ -122,6 +124,46 @@ def test_adaptive_all_keys_tied(F, S, k):
     want[:k] = True
     for h in range(Hq):
         assert np.array_equal(sel[0, h].astype(bool), want), f"head {h}"
+
+
+def test_adaptive_large_bucket_few_ties(F):
+    """One sign pattern for every key and per-key magnitudes within 3%: the
+    scores of a head fall into one or two first-digit buckets (more keys than
+    the final select holds in LDS) with a few hundred keys on each fp16 scale
+    value, so the threshold's ties (fewer than 512) are ranked by comparison
+    while the bucket is re-read from the lists.  The scenario is asserted on
+    the oracle's keys, then the selected sets must be bit-exact."""
+    say("case adaptive large bucket, few ties")
+    B, Hq, Hkv, S, d, k = 1, 4, 1, 16000, 128, 5000
+    rng = np.random.default_rng(1)
+    sign = np.where(rng.standard_normal(d) >= 0, 1.0, -1.0)
+    g = np.abs(rng.standard_normal(d)) + 0.5
+    a = 1.0 + 0.03 * rng.random(S)
+    kx = (a[:, None] * (sign * g)[None, :] * 0.05).astype(np.float16).reshape(B, Hkv, S, d)
+    q = (rng.standard_normal((B, Hq, d)) * 0.1).astype(np.float16)
+    vx = (rng.standard_normal((B, Hkv, S, d)) * 0.1).astype(np.float16)
+    Kb, Kr = O.encode_fused(kx.reshape(-1, d))
+    Vb, Vr = O.encode_fused(vx.reshape(-1, d))
+    # the scenario, on the oracle's ranking keys of head 0
+    pc = ((kx[0, 0] >= 0) == (q[0, 0] >= 0)).sum(1)
+    key = O.topk_key(Kb.scale, pc, d)
+    T = np.sort(key)[::-1][k - 1]
+    u = T.astype(np.float32).view(np.uint32)
+    ok = np.where(key.view(np.uint32) & 0x80000000, ~key.view(np.uint32), key.view(np.uint32) | 0x80000000)
+    ot = (~u) if (u & 0x80000000) else (u | 0x80000000)
+    in_bucket = int(((ok >> 19) == (ot >> 19)).sum())
+    ties = int((key == T).sum())
+    assert in_bucket > 6144 and 1 < ties <= 512, (in_bucket, ties)
+    kb, kr = F.encode_fused(torch.from_numpy(kx.reshape(-1, d)).cuda())
+    vb, vr = F.encode_fused(torch.from_numpy(vx.reshape(-1, d)).cuda())
+    out, sel = F.adaptive_attention(torch.from_numpy(q).cuda(), kb, kr, vb, vr, B, Hq, S, d,
+                                    n_kv_heads=Hkv, top_k=k, return_selected=True)
+    _, ref, sets = O.adaptive_attention(q, Kb, Kr, Vb, Vr, B, Hq, S, k, n_kv_heads=Hkv,
+                                        return_f32=True, return_sets=True)
+    sel = to_np(sel)
+    for (b, h), idx in sets.items():
+        assert np.array_equal(np.nonzero(sel[b, h])[0], idx), f"set differs at {(b, h)}"
+    close(to_np(out).astype(np.float32), ref, what="large bucket")
 
 
 def test_config_c5_sample(F):
