@@ -297,7 +297,7 @@ def bench_c5(args, torch, _C, W):
         "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": traffic_from_profiles("traffic_c2_c5_counters.md", "traffic_bytes_per_step_c5"),
-                     "kernel": "whole adaptive step (radix passes + attention), wall clock"},
+                     "kernel": "whole adaptive step (selection launches + attention), wall clock"},
         "full_compensated_us": round(wall_c * 1e6, 1),
     }
 
