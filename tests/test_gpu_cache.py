@@ -206,3 +206,36 @@ def test_append_attend_in_a_hip_graph():
         for t in range(T):
             assert torch.equal(got[t], want[t]), f"replay {rep}, step {t}"
         assert torch.equal(cache._k_res, want_k), f"replay {rep}: cache bytes"
+
+
+@pytest.mark.parametrize("max_seq", [3000, 3001])
+def test_bitcache_attend_adaptive_partly_filled(max_seq):
+    """BitCache.attend_adaptive on a partly filled GQA ring (2000 of max_seq
+    tokens): the selection passes and the attention read rows at the ring's
+    stride; max_seq 3000 takes the eight-key scale loads, 3001 (stride not a
+    multiple of 8) the per-key ones.  Sets bit-exact, outputs against the
+    oracle (online encode of each group's tokens)."""
+    from bitcache_amd import BitCache
+    say(f"case bitcache adaptive partly filled max_seq={max_seq}")
+    B, Hq, Hkv, d, S, top_k = 2, 8, 2, 128, 2000, 200
+    G = Hq // Hkv
+    rng = np.random.default_rng(max_seq)
+    k = (rng.standard_normal((B, Hkv, S, d)) * 0.2).astype(np.float16)
+    v = (rng.standard_normal((B, Hkv, S, d)) * 0.2).astype(np.float16)
+    q = (rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)
+    cache = BitCache(B, Hq, d, max_seq, n_kv_heads=Hkv)
+    cache.prefill(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    out, sel = cache.attend_adaptive(torch.from_numpy(q).cuda(), top_k=top_k, return_selected=True)
+    out, sel = to_np(out).astype(np.float32), to_np(sel)
+    assert sel.shape == (B, Hq, S)
+    for b in range(B):
+        for kvh in range(Hkv):
+            Kb, Kr = O.online_encode(k[b, kvh])
+            Vb, Vr = O.online_encode(v[b, kvh])
+            qg = q[b, kvh * G:(kvh + 1) * G][None]
+            _, ref, sets = O.adaptive_attention(qg, Kb, Kr, Vb, Vr, 1, G, S, top_k, n_kv_heads=1,
+                                                return_f32=True, return_sets=True)
+            for (_, h), want in sets.items():
+                got = np.nonzero(sel[b, kvh * G + h])[0]
+                assert np.array_equal(got, want), f"set differs at (b={b}, h={kvh * G + h})"
+            close(out[b, kvh * G:(kvh + 1) * G], ref[0], what=f"adaptive ring group {(b, kvh)}")
