@@ -860,7 +860,8 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
 // epilogue weigh more than the latency hiding of a third: c2 54.5 -> 52.9 us).
 int plan_per_cu(int mode, int D, int G) {
     if ((mode == MODE_COMP || mode == MODE_MIXED) && G == 1) return 0;
-    const int cap = mode == MODE_BINARY && G == 1 ? 2 : 3;
+    // (MHA binary 2, GQA binary 4, the other modes 3: measured)
+    const int cap = mode == MODE_BINARY ? (G == 1 ? 2 : 4) : 3;
     const int n = bc::mfma_wgs_per_cu(mode, D, G);
     return n <= 0 ? cap : (n < cap ? n : cap);
 }
