@@ -62,6 +62,10 @@ CASES = [
     (1, 8, 2, 40000, 128, 4000, False),
     (2, 4, 4, 12000, 64, 1, False),
     (1, 2, 2, 9000, 256, 8999, False),
+    # groups of 8 heads at long context (the selection's 8-head instances over
+    # many key chunks), with and without ties
+    (2, 16, 2, 40000, 128, 4000, False),
+    (1, 16, 2, 20000, 64, 2000, True),
 ]
 
 
