@@ -71,8 +71,6 @@ def cpu_baseline(q, kb, kr, vb, vr, B, H, S, d, budget_s):
 
     def head(b, h):
         lo = (b * H + h) * S
-        def sl(blob, per, scale_off):
-            return blob
         kbw = kb[lo * d // 8:(lo + S) * d // 8].cpu().view(torch.int32).view(S, d // 32)
         ks = kb[n * d // 8 + 2 * lo:n * d // 8 + 2 * (lo + S)].cpu().view(torch.float16)
         kc = kr[lo * d // 2:(lo + S) * d // 2].cpu().view(S, d // 2)
@@ -147,14 +145,14 @@ def bench_c2(args, torch, _C, W):
     cfg = W.CONFIGS["c2"]
     B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
     q, k, _ = W.make_c2(cfg)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(11)
+    v = W.make_c2_values(cfg)
     copies = []
     for i in range(3):
-        kk = k if i == 0 else (k.float() * -1.0 if i == 1 else k.float() * 0.5).half()
-        kb = _C.binary_encode(kk.view(-1, d))
-        vb = _C.binary_encode((torch.randn(kk.shape, generator=g, device="cuda") / 11.3).half().view(-1, d))
-        copies.append((kb, vb))
+        f = (1.0, -1.0, 0.5)[i]
+        kk = k if i == 0 else (k.float() * f).half()
+        vv = v if i == 0 else (v.float() * -f).half()
+        copies.append((_C.binary_encode(kk.view(-1, d)), _C.binary_encode(vv.view(-1, d))))
+    del v
     torch.cuda.synchronize()
     it = [0]
 

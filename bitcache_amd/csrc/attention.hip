@@ -804,12 +804,13 @@ struct SplitPlan {
 // per-CU speed differences of a long bandwidth-bound launch (measured faster
 // on the 64K-context MHA compensated step); a launch too small for two such
 // rounds fills one round of 3 workgroups per CU.
-SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
+// `cu` is the device's CU count (0: the current device's).
+SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu, int cu = 0) {
     SplitPlan p;
     p.G = pick_g(hq / hkv);
     const int64_t groups = (int64_t)batch * hkv * ((hq / hkv) / p.G);
     const int tiles = (S + 63) / 64;
-    const int cu = bc::device_cu_count();
+    if (cu <= 0) cu = bc::device_cu_count();
     int max_split = tiles / 8;                   // at least 8 tiles (2 per wave) per split
     if (max_split > kMaxSplits) max_split = kMaxSplits;   // the combine kernel's weight table
     if (max_split < 1) max_split = 1;
@@ -858,10 +859,16 @@ SplitPlan plan_splits(int batch, int hq, int hkv, int S, int per_cu) {
 // per CU (the adaptive kernel's LDS allows two at d = 128), binary attention
 // at most two (its tiles are short, so a workgroup's fixed prologue and
 // epilogue weigh more than the latency hiding of a third: c2 54.5 -> 52.9 us).
+//
+// kMaxPerCu bounds every policy: ws_bytes sizes the workspace over the plans
+// of per_cu = 0 .. kMaxPerCu, so a policy above it would launch more splits
+// than the workspace holds.
+constexpr int kMaxPerCu = 4;
 int plan_per_cu(int mode, int D, int G) {
     if ((mode == MODE_COMP || mode == MODE_MIXED) && G == 1) return 0;
     // (MHA binary 2, GQA binary 4, the other modes 3: measured)
-    const int cap = mode == MODE_BINARY ? (G == 1 ? 2 : 4) : 3;
+    int cap = mode == MODE_BINARY ? (G == 1 ? 2 : 4) : 3;
+    if (cap > kMaxPerCu) cap = kMaxPerCu;
     const int n = bc::mfma_wgs_per_cu(mode, D, G);
     return n <= 0 ? cap : (n < cap ? n : cap);
 }
@@ -879,14 +886,21 @@ bool valu_forced() {
     return forced;
 }
 
-// workspace of the split partials: the largest plan of any mode
-size_t ws_bytes(int batch, int hq, int hkv, int S, int D) {
-    int n = 1;
-    for (int per_cu = 0; per_cu <= 3; per_cu++) {
-        const SplitPlan p = plan_splits(batch, hq, hkv, S, per_cu);
-        n = p.n_splits > n ? p.n_splits : n;
+// bytes of the split partials a plan writes: one (max, sum, acc[D]) fp32
+// record per (b, query head, split)
+size_t plan_bytes(int batch, int hq, const SplitPlan& p, int D) {
+    return (size_t)batch * hq * p.n_splits * (D + 2) * sizeof(float);
+}
+
+// workspace of the split partials: the largest plan of any policy
+// plan_per_cu can return (per_cu = 0 .. kMaxPerCu)
+size_t ws_bytes(int batch, int hq, int hkv, int S, int D, int cu = 0) {
+    size_t n = plan_bytes(batch, hq, plan_splits(batch, hq, hkv, S, 0, cu), D);
+    for (int per_cu = 1; per_cu <= kMaxPerCu; per_cu++) {
+        const size_t b = plan_bytes(batch, hq, plan_splits(batch, hq, hkv, S, per_cu, cu), D);
+        n = b > n ? b : n;
     }
-    return (size_t)batch * hq * n * (D + 2) * sizeof(float);
+    return n;
 }
 
 int validate_heads(int batch, int n_heads, int n_kv_heads, int seq_len, int kv_stride, int d) {
@@ -966,6 +980,11 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
                "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
     const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu);
+    // (the bound the launch needs: the partials of the plan it runs)
+    const size_t plan_ws = plan_bytes(batch, n_heads, p, head_dim);
+    BC_REQUIRE(workspace_bytes >= plan_ws, BC_ERR_WORKSPACE,
+               "the split plan writes %zu bytes of partials, workspace holds %zu", plan_ws,
+               workspace_bytes);
     const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
     AttnArgs a{};
     a.q = (const uint16_t*)q;
@@ -1050,6 +1069,24 @@ extern "C" int bc_attention_workspace_size(int batch, int n_heads, int n_kv_head
     if (v != BC_OK) return v;
     BC_REQUIRE(bytes != nullptr, BC_ERR_INVALID_ARGUMENT, "null bytes");
     *bytes = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim);
+    return BC_OK;
+}
+
+extern "C" int bc_attention_split_plan(int mode, int batch, int n_heads, int n_kv_heads,
+                                       int seq_len, int head_dim, int cu_count, int* n_splits,
+                                       size_t* partial_bytes, size_t* workspace_bytes) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, seq_len, head_dim);
+    if (v != BC_OK) return v;
+    BC_REQUIRE(mode >= MODE_BINARY && mode <= MODE_MIXED, BC_ERR_INVALID_ARGUMENT,
+               "unknown attention mode %d", mode);
+    BC_REQUIRE(cu_count >= 0, BC_ERR_INVALID_ARGUMENT, "cu_count %d < 0", cu_count);
+    BC_REQUIRE(n_splits && partial_bytes && workspace_bytes, BC_ERR_INVALID_ARGUMENT,
+               "null output");
+    const int per_cu = plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads));
+    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu, cu_count);
+    *n_splits = p.n_splits;
+    *partial_bytes = plan_bytes(batch, n_heads, p, head_dim);
+    *workspace_bytes = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim, cu_count);
     return BC_OK;
 }
 

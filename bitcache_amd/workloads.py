@@ -92,6 +92,14 @@ def make_c2(cfg: Config = CONFIGS["c2"], device="cuda", seq_len=None):
     return q.half(), k.half().contiguous(), mask
 
 
+def make_c2_values(cfg: Config = CONFIGS["c2"], device="cuda", seq_len=None):
+    """V [B, H, S, d] for c2's binary attention: N(0, 1/128), seed cfg.seed + 10
+    (the configuration names no V distribution; scoring does not depend on it)."""
+    S = cfg.seq_len if seq_len is None else seq_len
+    g = _gen(device, cfg.seed + 10)
+    return normal((cfg.batch, cfg.n_heads, S, cfg.head_dim), g, device).half().contiguous()
+
+
 def algorithmic_bytes_per_key(d=D, residual=True):
     """Bytes of one K or V vector that attention must read: d/8 + 2 (+ d/2 + 2)."""
     return d // 8 + 2 + ((d // 2 + 2) if residual else 0)

@@ -140,6 +140,20 @@ int bc_read_probe(const void* src, int64_t n_bytes, void* out, void* stream);
 int bc_attention_workspace_size(int batch, int n_heads, int n_kv_heads, int seq_len,
                                 int head_dim, size_t* bytes);
 
+/* The key-split plan an attention call of this shape launches: n_splits per
+ * (b, query-head group), the bytes of split partials it writes and the
+ * workspace bc_attention_workspace_size reports (always >= partial_bytes).
+ * mode: BC_MODE_*; cu_count 0 plans for the current device, > 0 for a device
+ * of that many CUs.  Allocates nothing and launches nothing.  No counterpart
+ * in the reference; a diagnostic for callers sizing workspaces and for tests. */
+#define BC_MODE_BINARY 0
+#define BC_MODE_COMPENSATED 1
+#define BC_MODE_ADAPTIVE 2
+#define BC_MODE_HEAD_MODE 3
+int bc_attention_split_plan(int mode, int batch, int n_heads, int n_kv_heads, int seq_len,
+                            int head_dim, int cu_count, int* n_splits, size_t* partial_bytes,
+                            size_t* workspace_bytes);
+
 /* Binary-only decode attention, MHA, blob capacity batch*n_heads*seq_len.
  * Replaces launch_binary_attention (src/binary_attention.cu:84-105). */
 int bc_binary_attention(const void* q, const void* k_bin, const void* v_bin, void* out, int batch,

@@ -571,6 +571,108 @@ class RingState:
 # ----------------------------------------------------------------------------
 # torch-CPU fast path for the CPU baseline (same math, multi-threaded)
 # ----------------------------------------------------------------------------
+def _torch_sign_bytes(words):
+    """int64 view of u32 sign words [S, d/32] -> uint8 [S, d/8] (little-endian)."""
+    import torch
+    sh = torch.tensor([0, 8, 16, 24], dtype=torch.int64)
+    return ((words.unsqueeze(-1) >> sh) & 0xFF).to(torch.uint8).reshape(words.shape[0], -1)
+
+
+_POPC8 = None
+
+
+def _torch_popcounts(q32, kbytes):
+    """XNOR popcounts (src/xnor_dot.cuh:20-27) of query rows q32 [G, d] against
+    key sign bytes [S, d/8] -> int32 [G, S], by a 256-entry byte table."""
+    import torch
+    global _POPC8
+    if _POPC8 is None:
+        _POPC8 = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int32)
+    G, d = q32.shape
+    qbits = (q32 >= 0).to(torch.uint8).reshape(G, d // 8, 8)
+    qbytes = (qbits << torch.arange(8, dtype=torch.uint8)).sum(-1).to(torch.uint8)   # [G, d/8]
+    x = torch.bitwise_not(torch.bitwise_xor(kbytes.unsqueeze(0), qbytes.unsqueeze(1)))
+    return _POPC8[x.long()].sum(-1, dtype=torch.int32)
+
+
+def _torch_scale_q(q32):
+    """scale_q per row: sequential fp32 sum of |q_i|, / d (src/compensated_attention.cu:65-67)."""
+    import torch
+    d = q32.shape[-1]
+    sq = torch.zeros(q32.shape[0], dtype=torch.float32)
+    for i in range(d):
+        sq = sq + q32[:, i].abs()
+    return sq / d
+
+
+def _torch_vbin(vwords, vscale16, d):
+    """+-scale_v per element from the V sign words [S, d]."""
+    import torch
+    vb = _torch_sign_bytes(vwords)
+    bits = ((vb.unsqueeze(-1) >> torch.arange(8, dtype=torch.uint8)) & 1).reshape(vb.shape[0], d)
+    sv = vscale16.float().unsqueeze(1)
+    return torch.where(bits.bool(), sv, -sv)
+
+
+def _torch_softmax_out(sc, vrec):
+    """m = max(-1e38, s); w = exp(s - m); out = fp16((w @ vrec) / sum w), per row."""
+    import torch
+    m = torch.clamp(sc.max(dim=-1, keepdim=True).values, min=-1e38)
+    w = torch.exp(sc - m)
+    l = w.sum(-1, keepdim=True)
+    return ((w @ vrec) * (1.0 / l)).half()
+
+
+def binary_attention_torch_cpu(q16, kwords, kscale16, vwords, vscale16):
+    """Query rows q16 [G, d] over one kv head's S keys, binary attention on torch
+    CPU tensors (src/binary_attention.cu:24-81): score = (scale_q*scale_k) *
+    (2pc - d) * inv_sqrt_d, V = +-scale_v.  Words: int64 view of the u32 sign
+    words; scales fp16.  Returns fp16 [G, d]."""
+    d = q16.shape[-1]
+    q32 = q16.reshape(-1, d).float()
+    pc = _torch_popcounts(q32, _torch_sign_bytes(kwords))
+    xd = (_torch_scale_q(q32).unsqueeze(1) * kscale16.float().unsqueeze(0)) * (2 * pc - d).float()
+    return _torch_softmax_out(xd * float(inv_sqrt(d)), _torch_vbin(vwords, vscale16, d))
+
+
+def adaptive_attention_torch_cpu(q16, kwords, kscale16, kcodes, krscale16, vwords, vscale16,
+                                 vcodes, vrscale16, top_k):
+    """adaptive_attention for query rows q16 [G, d] sharing one kv head's S keys,
+    on torch CPU tensors: per row the top_k keys by topk_key (a stable sort on
+    -key: largest first, lowest index on ties; NaN last, -0 as +0) take the
+    compensated score and V, the others the binary ones; one softmax.  Returns
+    (fp16 [G, d], bool [G, S] selected)."""
+    import torch
+    d = q16.shape[-1]
+    q32 = q16.reshape(-1, d).float()
+    G, S = q32.shape[0], kwords.shape[0]
+    pc = _torch_popcounts(q32, _torch_sign_bytes(kwords))
+    n = (2 * pc - d).float()
+    xd = (_torch_scale_q(q32).unsqueeze(1) * kscale16.float().unsqueeze(0)) * n
+    key = kscale16.float().unsqueeze(0) * n + 0.0
+    key = torch.where(torch.isnan(key), torch.tensor(-math.inf), key)
+    k = min(top_k, S)
+    order = torch.sort(-key, dim=-1, stable=True).indices[:, :k]
+    sel = torch.zeros((G, S), dtype=torch.bool)
+    sel.scatter_(1, order, True)
+    isd = float(inv_sqrt(d))
+    vbin = _torch_vbin(vwords, vscale16, d)
+    out = torch.empty((G, d), dtype=torch.float16)
+    for g in range(G):
+        idx = order[g]
+        kdeq = (kcodes[idx].float() / 7.0) * krscale16[idx].float().unsqueeze(1)
+        sc = xd[g] * isd
+        sc[idx] = (xd[g, idx] + kdeq @ q32[g]) * isd
+        # softmax as _torch_softmax_out, with the V residual added on the
+        # selected rows only: sum_s w_s vbin_s + sum_{s in sel} w_s vres_s
+        m = torch.clamp(sc.max(), min=-1e38)
+        w = torch.exp(sc - m)
+        vdeq = (vcodes[idx].float() / 7.0) * vrscale16[idx].float().unsqueeze(1)
+        acc = w @ vbin + w[idx] @ vdeq
+        out[g] = (acc * (1.0 / w.sum())).half()
+    return out, sel
+
+
 def compensated_attention_torch_cpu(q16, kwords, kscale16, kcodes, krscale16,
                                     vwords, vscale16, vcodes, vrscale16):
     """One (b, head) of compensated attention on torch CPU tensors, vectorised.

@@ -95,6 +95,14 @@ def ring_oracle_keys(hist_k, max_seq, B, Hkv, d):
     return O.online_encode(ks.reshape(-1, d))[0], n
 
 
+def bin_head_tensors(bb, n, d, lo, S):
+    """S vectors from cache vector lo of a binary blob (capacity n) as torch-CPU
+    tensors: sign words (int64 view of the u32 words) and fp16 scales."""
+    w = bb[lo * d // 8:(lo + S) * d // 8].cpu().view(torch.int32).view(S, d // 32)
+    sc = bb[n * d // 8 + 2 * lo:n * d // 8 + 2 * (lo + S)].cpu().view(torch.float16)
+    return w.to(torch.int64) & 0xFFFFFFFF, sc
+
+
 def blob_head_tensors(kb, kr, vb, vr, n, d, lo, S):
     """One (b, head)'s S keys starting at cache vector lo, read from the
     device blobs (capacity n) as the torch-CPU tensors

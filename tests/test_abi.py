@@ -143,12 +143,58 @@ def test_attention_argument_errors(lib, no_gpu):
     assert h(*[fake] * 5, None, fake, 1, 4, 4, 100, 100, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
     assert h(fake, fake, None, fake, fake, modes, fake, 1, 4, 4, 100, 100, 128, fake, 1 << 30, None) == BC_ERR_INVALID_ARGUMENT
     assert h(*[fake] * 5, modes, fake, 1, 4, 4, 100, 100, 128, fake, 1, None) == BC_ERR_WORKSPACE
+    # the allocation-free entry point rejects a shape whose partials exceed
+    # its array before it looks the array up or launches anything
+    na = lib.bc_attention_gqa_noalloc
+    na.argtypes = [P] * 6 + [ctypes.c_int] * 6 + [P]
+    assert na(*[fake] * 6, 4096, 64, 8, 1 << 20, 1 << 20, 128, None) == BC_ERR_WORKSPACE
+    assert b"allocation-free" in lib.bc_last_error()
     e = lib.bc_compute_head_entropy_gqa
     e.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [P]
     assert e(fake, fake, fake, 1, 6, 4, 100, 100, 128, None) == BC_ERR_INVALID_ARGUMENT  # 6 % 4
     assert e(fake, fake, fake, 1, 4, 2, 100, 50, 128, None) == BC_ERR_INVALID_ARGUMENT   # stride < S
     assert e(fake, fake, None, 1, 4, 2, 100, 100, 128, None) == BC_ERR_INVALID_ARGUMENT  # null output
     assert e(fake, fake, fake, 1, 4, 2, 100, 100, 80, None) == BC_ERR_UNSUPPORTED
+
+
+def test_workspace_covers_every_split_plan(lib):
+    """The workspace bc_attention_workspace_size reports holds the split
+    partials of the plan every attention mode launches, on devices of several
+    CU counts (the plan depends on the CU count), over shapes where the
+    policies' split counts differ: MHA and GQA groups 1-8, short and long
+    contexts, the BASELINE shapes among them.  No launch: the plan is host
+    arithmetic.  (On a host without a GPU each mode plans at its largest
+    workgroups-per-CU policy, the case with the most splits.)"""
+    size_t = ctypes.c_size_t
+    f = lib.bc_attention_split_plan
+    f.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(size_t),
+                                       ctypes.POINTER(size_t)]
+    ws = lib.bc_attention_workspace_size
+    ws.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(size_t)]
+    shapes = [(8, 32, 32, 32768, 128), (8, 32, 32, 65536, 128), (4, 32, 8, 16384, 128),
+              (4, 32, 8, 16640, 128), (2, 32, 8, 32768, 128), (1, 32, 8, 65536, 128),
+              (16, 32, 8, 131072, 128), (1, 8, 1, 100000, 64), (3, 16, 2, 9000, 256),
+              (1, 4, 4, 700, 96), (2, 64, 8, 50000, 128), (1, 32, 16, 4096, 128),
+              (1, 1, 1, 1, 128), (1, 32, 8, 1 << 20, 128)]
+    n, part, total, ref = ctypes.c_int(0), size_t(0), size_t(0), size_t(0)
+    checked = 0
+    for (B, Hq, Hkv, S, d) in shapes:
+        for cu in (0, 80, 256, 304):
+            for mode in range(4):
+                assert f(mode, B, Hq, Hkv, S, d, cu, ctypes.byref(n), ctypes.byref(part),
+                         ctypes.byref(total)) == BC_OK, lib.bc_last_error()
+                assert 1 <= n.value <= 2048
+                assert part.value == B * Hq * n.value * (d + 2) * 4
+                assert part.value <= total.value, (
+                    f"mode {mode} shape {(B, Hq, Hkv, S, d)} cu {cu}: plan writes "
+                    f"{part.value} B, workspace {total.value} B")
+                checked += 1
+            if cu == 0:
+                assert ws(B, Hq, Hkv, S, d, ctypes.byref(ref)) == BC_OK
+                assert ref.value == total.value
+    assert checked == len(shapes) * 16
+    assert f(4, 1, 4, 4, 100, 128, 0, ctypes.byref(n), ctypes.byref(part),
+             ctypes.byref(total)) == BC_ERR_INVALID_ARGUMENT
 
 
 def test_extension_rejects_cpu_tensors():

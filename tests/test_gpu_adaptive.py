@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.gpu_util import bin_from_blob, close, res_from_blob, say, to_np
+from tests.gpu_util import bin_from_blob, blob_head_tensors, close, res_from_blob, say, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -204,8 +204,10 @@ def test_config_c5_full_size(F):
     above a selected one; keys equal to the threshold are taken lowest index
     first.  The ranking key scale_k * (2pc - d) comes from the GPU independently
     of the kernels under test: 2pc - d = sign(k) . sign(q) is an exact +-1
-    matmul in fp32 and the product with the fp16 scale is exact.  Two head
-    groups are also compared with the oracle (sets and outputs)."""
+    matmul in fp32 and the product with the fp16 scale is exact.  All 512
+    heads' sets and outputs are compared with the torch-CPU restatement of the
+    adaptive attention, and one head group with the numpy oracle from the fp16
+    inputs."""
     from bitcache_amd import workloads as W
     say("case c5 full size")
     cfg = W.CONFIGS["c5"]
@@ -235,18 +237,40 @@ def test_config_c5_full_size(F):
         last_sel = torch.where(s & (key == lo_sel[:, None]), idx, -1).amax(-1)
         first_uns = torch.where(~s & (key == lo_sel[:, None]), idx, S).amin(-1)
         assert bool((last_sel < first_uns)[tie].all()), f"ties not taken lowest index first, b={b}"
-    for b, kvh in [(0, 0), (15, 7)]:
-        Kb, Kr = O.encode_fused(to_np(k[b, kvh]))
-        Vb, Vr = O.encode_fused(to_np(v[b, kvh]))
-        qg = to_np(q[b, kvh * G:(kvh + 1) * G])[None]
-        _, ref, sets = O.adaptive_attention(qg, Kb, Kr, Vb, Vr, 1, G, S, top_k, n_kv_heads=1,
-                                            return_f32=True, return_sets=True)
-        for (_, h), want in sets.items():
-            got = np.nonzero(to_np(sel[b, kvh * G + h]))[0]
-            assert np.array_equal(got, want), f"set differs at (b={b}, h={kvh * G + h})"
-        close(to_np(out[b, kvh * G:(kvh + 1) * G]).astype(np.float32), ref[0],
-              what=f"c5 full size group {(b, kvh)}")
-    del q, k, v, kb, kr, vb, vr, out, sel
+    # one head group against the numpy oracle from the fp16 inputs (its own
+    # encode, selection and attention)
+    b, kvh = 15, 7
+    Kb, Kr = O.encode_fused(to_np(k[b, kvh]))
+    Vb, Vr = O.encode_fused(to_np(v[b, kvh]))
+    qg = to_np(q[b, kvh * G:(kvh + 1) * G])[None]
+    _, ref, sets = O.adaptive_attention(qg, Kb, Kr, Vb, Vr, 1, G, S, top_k, n_kv_heads=1,
+                                        return_f32=True, return_sets=True)
+    for (_, h), want in sets.items():
+        got = np.nonzero(to_np(sel[b, kvh * G + h]))[0]
+        assert np.array_equal(got, want), f"set differs at (b={b}, h={kvh * G + h})"
+    close(to_np(out[b, kvh * G:(kvh + 1) * G]).astype(np.float32), ref[0],
+          what=f"c5 full size group {(b, kvh)}")
+    del k, v
+    # every one of the 512 heads against the torch-CPU restatement of the
+    # adaptive attention on the same device blobs: the selected set bit for
+    # bit, the output at the north_star tolerance
+    torch.set_num_threads(min(16, len(__import__("os").sched_getaffinity(0))))
+    kbc, krc, vbc, vrc, qc = kb.cpu(), kr.cpu(), vb.cpu(), vr.cpu(), q.cpu()
+    selc = sel.cpu().bool()
+    got = to_np(out).astype(np.float32)
+    ref = np.empty((B, Hq, d), np.float32)
+    for b in range(B):
+        for kvh in range(Hkv):
+            args = blob_head_tensors(kbc, krc, vbc, vrc, n, d, (b * Hkv + kvh) * S, S)
+            o, s = O.adaptive_attention_torch_cpu(qc[b, kvh * G:(kvh + 1) * G], *args, top_k)
+            assert torch.equal(s, selc[b, kvh * G:(kvh + 1) * G]), f"set differs in group {(b, kvh)}"
+            ref[b, kvh * G:(kvh + 1) * G] = o.float().numpy()
+        say(f"  c5 batch {b}: sets and outputs checked")
+    close(got, ref, what="c5 all heads")
+    cosh = (got * ref).sum(-1) / (np.linalg.norm(got, axis=-1) * np.linalg.norm(ref, axis=-1))
+    say(f"c5 all 512 heads vs torch-CPU restatement: min cosine {cosh.min():.7f}")
+    assert cosh.min() >= 0.9999
+    del q, kb, kr, vb, vr, out, sel
     torch.cuda.empty_cache()
 
 

@@ -9,8 +9,8 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.gpu_util import (assert_same_bin, assert_same_res, bin_from_blob, blob_head_tensors, close,
-                            res_from_blob, say, slice_enc, to_np)
+from tests.gpu_util import (assert_same_bin, assert_same_res, bin_from_blob, bin_head_tensors,
+                            blob_head_tensors, close, res_from_blob, say, slice_enc, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -274,6 +274,53 @@ def test_config_c2_full_size_scores(F):
     say(f"c2 Kendall tau over {len(taus)} heads: tau-a mean {taus[:, 0].mean():.4f} "
         f"min {taus[:, 0].min():.4f}; tau-b mean {taus[:, 1].mean():.4f} min {taus[:, 1].min():.4f}")
     assert taus[:, 1].min() > 0.2 and np.all(taus[:, 0] <= taus[:, 1] + 1e-12)
+    del sq, sk, dots, exact
+    # binary attention on c2's inputs (the correlated-key softmax regime), all
+    # 256 heads against the torch-CPU restatement of the reference's binary
+    # attention (src/binary_attention.cu:8-82) on the same device blobs
+    v = W.make_c2_values(cfg)
+    vb = F.encode(v.view(-1, d))
+    out = F.binary_attention(q, kb, vb, B, H, S, d)
+    torch.cuda.synchronize()
+    torch.set_num_threads(min(16, len(__import__("os").sched_getaffinity(0))))
+    n = B * H * S
+    kbc, vbc, qc = kb.cpu(), vb.cpu(), q.cpu()
+    ref = np.empty((B, H, d), np.float32)
+    for b in range(B):
+        for h in range(H):
+            kw, ks = bin_head_tensors(kbc, n, d, (b * H + h) * S, S)
+            vw, vs = bin_head_tensors(vbc, n, d, (b * H + h) * S, S)
+            ref[b, h] = O.binary_attention_torch_cpu(qc[b, h][None], kw, ks, vw, vs)[0].float().numpy()
+    got = to_np(out).astype(np.float32)
+    close(got, ref, what="c2 binary attention, all heads")
+    cosh = (got * ref).sum(-1) / (np.linalg.norm(got, axis=-1) * np.linalg.norm(ref, axis=-1))
+    say(f"c2 binary attention, all 256 heads vs torch-CPU restatement: min cosine {cosh.min():.7f}")
+    assert cosh.min() >= 0.9999
+
+
+def test_fp32_order_kats(F):
+    """Hand-derived known answers on the GPU (derivations in
+    tests/test_oracle.py): the encode scale's 128-lane tree order (d = 128:
+    fp16 0x2001; d = 64: 0x2401; a sequential sum gives 0x2000 / 0x2400), the
+    sequential scale_q (score = inv_sqrt(128) exactly = 0x3DB504F3; the tree
+    order or a reversed sum move it), and the association
+    (scale_q*scale_k)*(2pc-d) of the binary score (0x3F07E5AA; the other
+    association gives 0x3F07E5AB)."""
+    say("case fp32 order KATs")
+    for d, want in ((128, 0x2001), (64, 0x2401)):
+        x = np.array([[1.0, 2.0 ** -11] + [2.0 ** -24] * (d - 2)] * 3, np.float16)
+        x[1] *= -1
+        kb = F.encode(torch.from_numpy(x).cuda())
+        got = bin_from_blob(kb, 3, d).scale.view(np.uint16)
+        assert list(got) == [want] * 3, (d, [hex(g) for g in got])
+    c = 1 + 2.0 ** -10
+    q = np.array([[[1.0] + [2.0 ** -24] * 127], [[127.0, 1.0, 3 * 2.0 ** -16] + [0.0] * 125]],
+                 np.float16)                                    # [B=2, H=1, 128]
+    k = np.array([[1.0] * 128, [c] * 67 + [-c] * 61], np.float16)   # one key per batch
+    kb = F.encode(torch.from_numpy(k).cuda())
+    sc, pc = F.binary_scores(torch.from_numpy(q).cuda(), kb, 2, 1, 1, 128)
+    assert list(to_np(pc).reshape(-1)) == [128, 67]
+    assert [hex(v) for v in to_np(sc).reshape(-1).view(np.uint32)] == ["0x3db504f3", "0x3f07e5aa"]
 
 
 def test_config_c3_full_size(F):

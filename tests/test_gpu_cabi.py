@@ -119,3 +119,52 @@ def test_cabi_append_attention_matches_bitcache(lib):
     for x, y in ((kb, ref._k_bin), (vb, ref._v_bin), (kr, ref._k_res), (vr, ref._v_res)):
         assert torch.equal(x, y)
     assert np.isfinite(out.float().cpu().numpy()).all()
+
+
+def test_split_partials_stay_inside_the_reported_workspace(lib):
+    """Regression: every attention mode's split plan writes its partials inside
+    the workspace bc_attention_workspace_size reports.  Binary GQA plans the
+    most workgroups per CU; at these shapes its plan holds more splits than a
+    workspace sized over fewer policies.  The workspace is the reported size
+    followed by a guard region of known bytes that must come back untouched,
+    and each output equals the operator module's."""
+    from bitcache_amd import _C
+    L = lib
+    L.bc_attention_split_plan.argtypes = [I32] * 7 + [ctypes.POINTER(I32), ctypes.POINTER(SZ),
+                                                      ctypes.POINTER(SZ)]
+    L.bc_head_mode_attention.argtypes = [P] * 7 + [I32] * 6 + [P, SZ, P]
+    guard = 1 << 20
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    for (B, Hq, Hkv, S, d) in [(4, 32, 8, 16384, 128), (2, 32, 8, 32768, 128),
+                               (1, 32, 8, 65536, 128)]:
+        say(f"case workspace guard B={B} Hq={Hq} Hkv={Hkv} S={S} d={d}")
+        n = B * Hkv * S
+        q = (torch.randn((B, Hq, d), generator=g, device="cuda") * 0.2).half()
+        kb, kr = _C.encode_fused((torch.randn((n, d), generator=g, device="cuda") * 0.2).half(), False)
+        vb, vr = _C.encode_fused((torch.randn((n, d), generator=g, device="cuda") * 0.2).half(), False)
+        modes = (torch.arange(B * Hq, device="cuda") % 3 == 0).to(torch.uint8)
+        nws = SZ(0)
+        ok(L, L.bc_attention_workspace_size(B, Hq, Hkv, S, d, ctypes.byref(nws)))
+        for mode in (0, 1, 3):
+            ns, part, total = I32(0), SZ(0), SZ(0)
+            ok(L, L.bc_attention_split_plan(mode, B, Hq, Hkv, S, d, 0, ctypes.byref(ns),
+                                            ctypes.byref(part), ctypes.byref(total)))
+            assert total.value == nws.value and part.value <= nws.value, (mode, ns.value)
+            ws = torch.full((nws.value + guard,), 0xA5, dtype=torch.uint8, device="cuda")
+            out = torch.empty((B, Hq, d), dtype=torch.float16, device="cuda")
+            if mode == 3:
+                ok(L, L.bc_head_mode_attention(ptr(q), ptr(kb), ptr(kr), ptr(vb), ptr(vr),
+                                               ptr(modes), ptr(out), B, Hq, Hkv, S, S, d, ptr(ws),
+                                               nws.value, stream()))
+                want = _C.head_mode_attention(q, kb, kr, vb, vr, modes, B, Hq, Hkv, S, S, d)
+            else:
+                kr_, vr_ = (kr, vr) if mode == 1 else (None, None)
+                ok(L, L.bc_attention_gqa(ptr(q), ptr(kb), P(kr_.data_ptr()) if mode else None,
+                                         ptr(vb), P(vr_.data_ptr()) if mode else None, ptr(out), B,
+                                         Hq, Hkv, S, S, d, ptr(ws), nws.value, stream()))
+                want = _C.attention(q, kb, kr_, vb, vr_, B, Hq, Hkv, S, S, d)
+            torch.cuda.synchronize()
+            tail = ws[nws.value:]
+            assert bool((tail == 0xA5).all()), f"mode {mode}: partials written past the workspace"
+            assert torch.equal(out, want), f"mode {mode}"

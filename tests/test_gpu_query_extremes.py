@@ -4,10 +4,12 @@ massive-activation channels of real decoder queries), fp16 extremes near
 65504, fp16 subnormals, and signed zeros.
 
 The matrix-core kernels take the INT4 residual dot q . dequant(K_res) on the
-stored nibbles with the query as 16-bit fixed point (q_int = rint(q / delta),
-delta = max|q| / 30583), where the reference sums q * (n/7 * s) in fp32
-(src/compensated_attention.cu:29-37).  The rounding error per element is at
-most delta/2 = max|q| / 61166, the same absolute bound on every element, so
+stored nibbles with the query as 24-bit fixed point (q_int = rint(q / step),
+step = max|q| / 7,800,000), where the reference sums q * (n/7 * s) in fp32
+(src/compensated_attention.cu:29-37).  A tile uses the top 16 bits unless a
+key's residual scale lets that truncation move its score by more than 2^-11
+nats, in which case it also adds the low 8 bits.  The rounding error per
+element is then at most step/2, the same absolute bound on every element, so
 elements far below max|q| keep fewer significant bits; these cases bound what
 that costs on the outputs: compensated MHA and GQA, adaptive top-k (whose
 selection uses only the exact binary key) and per-head modes, at d = 64, 128

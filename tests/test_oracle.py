@@ -7,6 +7,7 @@ answers, closed forms and brute force on tiny inputs.
 """
 import math
 import os
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -89,6 +90,133 @@ def test_scale_tree_order_differs_from_sequential():
     assert differs.any()          # the order is observable
     w, s, m = C.binary_encode(x)
     assert np.array_equal(m.view(np.uint32), b.mean32.view(np.uint32))
+
+
+# ---------------------------------------------------------------- fp32 order KATs
+# Hand-derived known answers for the three fp32 operation orders that fix the
+# encoded bytes and the binary scores.  Each input is chosen so that the
+# reference's order and the plausible alternatives round to different fp32
+# bits; the expected bits are worked out by hand in the comments (ulp(1) =
+# 2^-23 in fp32, 2^-10 in fp16; ties round to even).
+
+def _bits(v) -> int:
+    return int(np.asarray(v, np.float32).view(np.uint32))
+
+
+def _f32_round(x: Fraction) -> np.float32:
+    """Exact round-to-nearest-even of a rational to fp32 (normal range)."""
+    if x == 0:
+        return np.float32(0.0)
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** (e - 23)
+    n, rem = divmod(a, ulp)
+    n = int(n)
+    if rem / ulp > Fraction(1, 2) or (rem / ulp == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return np.float32(float((1 if x > 0 else -1) * n * ulp))
+
+
+def test_encode_scale_tree_order_kat():
+    """src/binary_encode.cu:31-53: 128 threads, p_t = |x_t| (+ |x_{t+128}|),
+    then p_t += p_{t+s} for s = 64 .. 1.
+
+    d = 128, x = [1, 2^-11, 2^-24 x 126].  Tree: s=64 gives p0 = 1 + 2^-24 ->
+    1 (tie, even), p1 = 2^-11 + 2^-24, p2..63 = 2^-23; each later level adds
+    a doubled power of two to p0 and p1 exactly, so before s=1 p0 = 1 +
+    31*2^-23 and p1 = 2^-11 + 63*2^-24; s=1 gives 1 + 2^-11 + 62.5*2^-23 ->
+    1 + 2^-11 + 62*2^-23 (tie, even mantissa 4158).  mean = that / 128 =
+    0x3C00103E; fp16 of it lies above the midpoint 2^-7*(1 + 2^-11), so the
+    scale is 2^-7*(1 + 2^-10) = 0x2001.
+    A left-to-right sum keeps 1 + 2^-11 (each + 2^-24 is a tie to even),
+    mean 2^-7*(1 + 2^-11), fp16 tie -> 0x2000.  An exact sum gives
+    1 + 2^-11 + 63*2^-23 (mean 0x3C00103F).
+    d = 64, x = [1, 2^-11, 2^-24 x 62]: p0 = 1 + 15*2^-23, p1 = 2^-11 +
+    31*2^-24 before s=1, total 1 + 2^-11 + 30*2^-23 (tie at 30.5, even),
+    mean 0x3C80101E, scale 2^-6*(1 + 2^-10) = 0x2401 (left to right: 0x2400)."""
+    for d, mean_bits, scale_bits, seq_scale in ((128, 0x3C00103E, 0x2001, 0x2000),
+                                                (64, 0x3C80101E, 0x2401, 0x2400)):
+        row = [1.0, 2.0 ** -11] + [2.0 ** -24] * (d - 2)
+        for sign in (1.0, -1.0):                # |x|: the signs must not matter
+            x = (np.array([row], np.float32) * sign).astype(np.float16)
+            b = O.binary_encode(x)
+            assert _bits(b.mean32[0]) == mean_bits, (d, hex(_bits(b.mean32[0])))
+            assert int(b.scale.view(np.uint16)[0]) == scale_bits
+            _, _, m = C.binary_encode(x)
+            assert _bits(m[0]) == mean_bits
+        # the alternatives named above round differently
+        seq = np.float32(0.0)
+        for v in row:
+            seq = np.float32(seq + np.float32(v))
+        assert int(np.float16(seq / np.float32(d)).view(np.uint16)) == seq_scale != scale_bits
+        exact = _f32_round(sum(Fraction(v) for v in row) / d)
+        assert _bits(exact) != mean_bits
+
+
+def test_scale_q_sequential_order_kat():
+    """src/compensated_attention.cu:65-67 (and binary_attention.cu:34-36):
+    scale_q = (sequential fp32 sum of |q_i|) / d; src/adaptive_precision.cu:46-59
+    (entropy) uses the encode's tree order instead.
+
+    d = 128, q = [1, 2^-24 x 127].  Left to right every + 2^-24 is a tie that
+    rounds back to 1, so scale_q = 2^-7 = 0x3C000000.  Tree order (as in the
+    encode KAT): 1 + (1+2+4+8+16+32)*2^-23 = 1 + 63*2^-23, scale 0x3C00003F.
+    Right to left: 127*2^-24 exactly, then + 1 -> 1 + 63.5*2^-23 -> 1 +
+    64*2^-23 (tie, even), 0x3C000040.
+    With a key of all-positive signs and scale 1 (popcount 128) the binary
+    score is (2^-7 * 1) * 128 * inv_sqrt_d = inv_sqrt_d exactly."""
+    q = np.array([[1.0] + [2.0 ** -24] * 127], np.float16)
+    _, sq, _ = O.query_prep(q)
+    _, sqt, _ = O.query_prep_tree(q)
+    assert _bits(sq[0]) == 0x3C000000
+    assert _bits(sqt[0]) == 0x3C00003F
+    rev = np.float32(0.0)
+    for v in q[0, ::-1].astype(np.float32):
+        rev = np.float32(rev + v)
+    assert _bits(rev / np.float32(128)) == 0x3C000040
+    _, csq = C.query_prep(q)
+    _, csqt = C.query_prep(q, tree=True)
+    assert _bits(csq[0]) == 0x3C000000 and _bits(csqt[0]) == 0x3C00003F
+    k = np.ones((1, 128), np.float16)
+    s = O.binary_scores(q.reshape(1, 1, 128), O.binary_encode(k), 1, 1, 1)
+    assert _bits(s[0, 0, 0]) == _bits(O.inv_sqrt(128)) == 0x3DB504F3
+
+
+def test_xnor_score_association_kat():
+    """src/xnor_dot.cuh:28-30: xdot = (scale_q * scale_k) * (float)(2pc - d).
+
+    scale_q = 1 + 3*2^-23, scale_k = 1 + 2^-10 (fp16), 2pc - d = 6.
+    (scale_q*scale_k) = 1 + 2^-10 + 3*2^-23 (+ 3*2^-33, dropped); times 6 =
+    6 + 6*2^-10 + 18*2^-23: at exponent 2 the ulp is 2^-21, so the tail is
+    4.5 ulps -> 4 (tie, even): 6 + 6*2^-10 + 2^-19 = 0x40C03004.
+    scale_q * (scale_k*6) rounds only once, from 4.5 ulps + 18*2^-33 (above
+    the tie) -> 5 ulps: 0x40C03005.
+    End to end: q = [127, 1, 3*2^-16, 0 x 125] gives the sequential sum
+    128 + 3*2^-16 (exact) and scale_q = 0x3F800003; the key [+c x 67,
+    -c x 61] with c = 1 + 2^-10 has scale c (0x3C01) and popcount 67, so
+    the score is fp32(0x40C03004 * inv_sqrt(128)) = 0x3F07E5AA."""
+    sq = np.float32(1 + 3 * 2.0 ** -23)
+    sk = np.array([1 + 2.0 ** -10], np.float16)
+    xd = O.xnor_dot(sq, np.array([67], np.int32), sk, 128)
+    assert _bits(xd[0]) == 0x40C03004
+    other = np.float32(sq * np.float32(np.float32(sk[0]) * np.float32(6)))
+    assert _bits(other) == 0x40C03005
+    fr = Fraction(float(sq)) * Fraction(float(sk[0]))
+    assert _bits(_f32_round(Fraction(float(_f32_round(fr))) * 6)) == 0x40C03004
+    q = np.array([[127.0, 1.0, 3 * 2.0 ** -16] + [0.0] * 125], np.float16)
+    _, sqq, _ = O.query_prep(q)
+    assert _bits(sqq[0]) == 0x3F800003
+    c = 1 + 2.0 ** -10
+    kb = O.binary_encode(np.array([[c] * 67 + [-c] * 61], np.float16))
+    assert int(kb.scale.view(np.uint16)[0]) == 0x3C01
+    s = O.binary_scores(q.reshape(1, 1, 128), kb, 1, 1, 1)
+    assert _bits(s[0, 0, 0]) == 0x3F07E5AA
+    assert _bits(_f32_round(Fraction(float(xd[0])) * Fraction(float(O.inv_sqrt(128))))) == 0x3F07E5AA
+    qw, csq = C.query_prep(q)
+    pc, cxd = C.xnor_scores(qw[0], float(csq[0]), kb.words, kb.scale, 128)
+    assert pc[0] == 67 and _bits(cxd[0]) == 0x40C03004
 
 
 def test_residual_kats():
@@ -282,6 +410,54 @@ def test_torch_cpu_restatement_matches_oracle():
                                rtol=2e-3, atol=2e-4)
 
 
+def test_torch_cpu_binary_and_adaptive_restatements_match_oracle():
+    """binary_attention_torch_cpu and adaptive_attention_torch_cpu (the fast
+    paths of the full-size c2 and c5 GPU checks) against the numpy oracle on
+    the same encodings: GQA rows sharing a kv head, repeated key rows so that
+    the top-k threshold falls inside tie groups, and a NaN / -0 / +inf K
+    scale for the selection's ordering rules.  Sets must be equal; outputs
+    agree to fp16 rounding."""
+    import torch
+    rng = np.random.default_rng(31)
+    d, S, G = 128, 700, 4
+    Q = (rng.standard_normal((1, G, d)) * 0.2).astype(np.float16)
+    base = (rng.standard_normal((S // 3, d)) * 0.2).astype(np.float16)
+    K = base[rng.integers(0, base.shape[0], S)]
+    V = (rng.standard_normal((S, d)) * 0.2).astype(np.float16)
+    Kb, Kr = O.encode_fused(K)
+    Vb, Vr = O.encode_fused(V)
+    w64 = lambda w: torch.from_numpy(w.astype(np.int64))
+    t = torch.from_numpy
+    args_k = (w64(Kb.words), t(Kb.scale))
+    args_v = (w64(Vb.words), t(Vb.scale))
+    _, ref = O.binary_attention(Q, Kb, Vb, 1, G, S, n_kv_heads=1, return_f32=True)
+    got = O.binary_attention_torch_cpu(t(Q[0]), *args_k, *args_v)
+    np.testing.assert_allclose(got.float().numpy(), ref[0].astype(np.float16).astype(np.float32),
+                               rtol=2e-3, atol=2e-4)
+    for top_k in (1, 70, 233, S - 1):
+        _, ref, sets = O.adaptive_attention(Q, Kb, Kr, Vb, Vr, 1, G, S, top_k, n_kv_heads=1,
+                                            return_f32=True, return_sets=True)
+        got, sel = O.adaptive_attention_torch_cpu(
+            t(Q[0]), *args_k, t(Kr.codes.astype(np.int8)), t(Kr.scale), *args_v,
+            t(Vr.codes.astype(np.int8)), t(Vr.scale), top_k)
+        for h in range(G):
+            assert np.array_equal(np.flatnonzero(sel[h].numpy()), sets[(0, h)]), (top_k, h)
+        np.testing.assert_allclose(got.float().numpy(), ref[0].astype(np.float16).astype(np.float32),
+                                   rtol=2e-3, atol=2e-4)
+    # special scales: the selection's ordering only (outputs are not finite)
+    ks = Kb.scale.copy()
+    ks[[3, 10, 11, 50]] = np.array([np.nan, -0.0, np.inf, 0.0], np.float16)
+    Kb2 = O.BinaryEnc(Kb.words, ks, ks.astype(np.float32))
+    with np.errstate(all="ignore"):
+        _, _, sets = O.adaptive_attention(Q, Kb2, Kr, Vb, Vr, 1, G, S, 90, n_kv_heads=1,
+                                          return_f32=True, return_sets=True)
+        _, sel = O.adaptive_attention_torch_cpu(
+            t(Q[0]), w64(Kb2.words), t(ks), t(Kr.codes.astype(np.int8)), t(Kr.scale), *args_v,
+            t(Vr.codes.astype(np.int8)), t(Vr.scale), 90)
+    for h in range(G):
+        assert np.array_equal(np.flatnonzero(sel[h].numpy()), sets[(0, h)]), h
+
+
 def test_attention_special_cases():
     rng = np.random.default_rng(9)
     d = 64
@@ -397,6 +573,69 @@ def test_adaptive_all_selected_equals_compensated_and_none_equals_binary():
     _, a0 = O.adaptive_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, 0, n_kv_heads=Hkv, return_f32=True)
     _, b0 = O.binary_attention(Q, Kb, Vb, B, Hq, S, n_kv_heads=Hkv, return_f32=True)
     np.testing.assert_allclose(a0, b0, rtol=1e-6, atol=1e-7)
+
+
+def test_adaptive_attention_closed_form_between_the_limits():
+    """O.adaptive_attention at 0 < k < S, MHA and GQA, with ties at the
+    threshold, against a float64 closed form built from the raw inputs: the
+    selected set by a lexsort on scale_k * (sgn q . sgn k) (largest first,
+    lowest index on ties), the score sq*sk*(sgn q . sgn k)/sqrt(d) plus, for
+    selected keys only, q . deq(K_res)/sqrt(d), and V = +-sv plus, for
+    selected keys only, deq(V_res).  A slip that pairs residual rows with the
+    wrong keys (first k rows, a transposed index, another head's set) moves
+    the output.  Intent: src/adaptive_precision.cuh:6-12; score
+    src/xnor_dot.cuh:30."""
+    rng = np.random.default_rng(29)
+    d = 128
+    for B, Hq, Hkv, S in ((1, 3, 3, 300), (2, 4, 2, 260)):
+        n = B * Hkv * S
+        # few distinct rows repeated in random order: many keys tie exactly
+        base = (rng.standard_normal((n // 4, d)) * 0.3).astype(np.float16)
+        K = base[rng.integers(0, base.shape[0], n)]
+        V = (rng.standard_normal((n, d)) * 0.3).astype(np.float16)
+        Q = (rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)
+        Kb, Kr = O.encode_fused(K)
+        Vb, Vr = O.encode_fused(V)
+        sgn = lambda a: np.where(a.astype(np.float64) >= 0, 1.0, -1.0)
+        sk = Kb.scale.astype(np.float64).reshape(B, Hkv, S)
+        kres = (Kr.codes.astype(np.float64) / 7 * Kr.scale.astype(np.float64)[:, None]).reshape(B, Hkv, S, d)
+        vres = (Vr.codes.astype(np.float64) / 7 * Vr.scale.astype(np.float64)[:, None]).reshape(B, Hkv, S, d)
+        vbin = (sgn(V) * Vb.scale.astype(np.float64)[:, None]).reshape(B, Hkv, S, d)
+        ksg = sgn(K).reshape(B, Hkv, S, d)
+        g = Hq // Hkv
+        keys = {}
+        for b in range(B):
+            for h in range(Hq):
+                keys[(b, h)] = sk[b, h // g] * (ksg[b, h // g] @ sgn(Q[b, h]))
+        # a k whose threshold falls inside a tie group of the first head
+        order0 = np.lexsort((np.arange(S), -keys[(0, 0)]))
+        kv = keys[(0, 0)][order0]
+        top_k = next(k for k in range(S // 10, S - 1) if kv[k - 1] == kv[k])
+        straddles = 0
+        out, o32, sets = O.adaptive_attention(Q, Kb, Kr, Vb, Vr, B, Hq, S, top_k, n_kv_heads=Hkv,
+                                              return_f32=True, return_sets=True)
+        for b in range(B):
+            for h in range(Hq):
+                key = keys[(b, h)]
+                order = np.lexsort((np.arange(S), -key))
+                sel = np.zeros(S, bool)
+                sel[order[:top_k]] = True
+                straddles += key[order[top_k - 1]] == key[order[top_k]]
+                assert np.array_equal(np.flatnonzero(sel), sets[(b, h)]), (b, h)
+                assert not np.array_equal(np.flatnonzero(sel), np.arange(top_k))
+                q = Q[b, h].astype(np.float64)
+                sq = np.abs(q).mean()
+                sc = (sq * key + sel * (kres[b, h // g] @ q)) / math.sqrt(d)
+                vrec = vbin[b, h // g] + sel[:, None] * vres[b, h // g]
+                w = np.exp(sc - sc.max())
+                ref = (w @ vrec) / w.sum()
+                np.testing.assert_allclose(o32[b, h], ref, rtol=1e-4, atol=2e-6 * np.abs(ref).max())
+                # the residual terms matter at this k: the binary-only and
+                # fully compensated outputs differ from the adaptive one
+                scb = sq * key / math.sqrt(d)
+                wb = np.exp(scb - scb.max())
+                assert np.abs((wb @ vbin[b, h // g]) / wb.sum() - ref).max() > 50 * 1e-4 * np.abs(ref).max()
+        assert straddles >= 1
 
 
 def test_ring_state():
