@@ -12,7 +12,7 @@ the stream it runs on; cpu_baseline = the CPU oracle (PyTorch-CPU
 restatement) on a bounded sample of the same heads, extrapolated to a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fp16]
-       python bench.py --config c2|c4|c5|prefill   (one line for another
+       python bench.py --config c2|c4|c5|mixed|prefill   (one line for another
        workload; the headline and the driver's line is the default c3)
 """
 from __future__ import annotations
@@ -38,11 +38,12 @@ def parse():
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 reference kernel")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5", "prefill"],
+    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5", "mixed", "prefill"],
                     help="workload (default c3, the headline; prefill: the encoders of the c3 cache)")
     ap.add_argument("--probe", action="store_true",
                     help="counter pass for rocprofv3 --pmc: one 1 GiB device copy (calibration) "
-                         "then --steps attention steps, no timing output")
+                         "then --steps attention steps, fp16 reference steps (unless --no-fp16) "
+                         "and head-entropy launches, no timing output")
     return ap.parse_args()
 
 
@@ -239,6 +240,15 @@ def bench_c4(args, torch, _C, W, bitcache_amd):
     two_call = sorted(loop(False) for _ in range(3))[1]
     per_key = 2 * W.algorithmic_bytes_per_key(d)
     alg = sum(B * Hkv * (S + t + 1) * per_key for t in range(T))
+    # the 89 MB a step reads fits the 256 MB last-level cache: its ceiling is
+    # one warm read of that many bytes (bc_read_probe, the attention kernels'
+    # load policy, one launch like the step's attention launch), not HBM
+    nb = (alg // T) // 16 * 16
+    buf = torch.ones(nb, dtype=torch.uint8, device="cuda")
+    _C.read_probe(buf)
+    llc_ms = event_ms(lambda: _C.read_probe(buf), 20, torch)
+    del buf
+    llc = nb / (llc_ms * 1e-3) / 1e9
     return {
         "metric": "online encode + decode loop tokens/s, GQA 32/8, 16K prefill + 256 steps, d=128, batch 4",
         "value": round(B * T / el, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -251,8 +261,12 @@ def bench_c4(args, torch, _C, W, bitcache_amd):
                    "batch": B, "heads": Hq, "kv_heads": Hkv, "prefill": S, "decode_steps": T,
                    "head_dim": d, "cache_bytes_per_step_avg": alg // T},
         "roofline": {"bound": "hbm", "achieved": round(alg / el / 1e9, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(alg / el / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(alg / el / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_profiles("attn_mfma_kernel_c4_counters.md", "traffic_bytes_per_step_c4"),
                      "kernel": "whole step incl. host launch overhead (cache is last-level-cache resident)"},
+        "llc_read_ceiling": {"bytes": nb, "us": round(llc_ms * 1e3, 1), "gbps": round(llc, 1),
+                             "step_frac_of_ceiling": round(alg / el / 1e9 / llc, 4),
+                             "what": "one warm read of a step's cache bytes (bc_read_probe, one launch)"},
     }
 
 
@@ -297,6 +311,54 @@ def bench_c5(args, torch, _C, W):
                      "traffic": traffic_from_profiles("traffic_c2_c5_counters.md", "traffic_bytes_per_step_c5"),
                      "kernel": "whole adaptive step (selection launches + attention), wall clock"},
         "full_compensated_us": round(wall_c * 1e6, 1),
+    }
+
+
+def bench_mixed(args, torch, _C, W):
+    """Per-head binary / compensated dispatch on the c3 cache (row f4, the
+    reference's adaptive-precision intent, src/adaptive_precision.cuh:25-31):
+    each head's mode from the entropy of its binary scores against the median
+    (bc_adaptive_select), so about half the heads are binary; a binary head
+    reads only the sign planes (18 B per key and side at d = 128) and a
+    compensated head all four (84 B).  Timed beside compensated attention of
+    the same cache in the same run."""
+    cfg = W.CONFIGS["c3"]
+    B, H, S, d = cfg.batch, cfg.n_heads, cfg.seq_len, cfg.head_dim
+    q, k, v = W.make_qkv(cfg)
+    kb, kr = _C.encode_fused(k.view(-1, d), False)
+    del k
+    vb, vr = _C.encode_fused(v.view(-1, d), False)
+    del v
+    ent = _C.compute_head_entropy(q, kb, B, H, S, d)
+    modes = _C.adaptive_select(ent, float(ent.median().item()))
+    torch.cuda.synchronize()
+    n_comp = int(modes.sum().item())
+    n_bin = B * H - n_comp
+
+    def step():
+        return _C.head_mode_attention(q, kb, kr, vb, vr, modes, B, H, H, S, S, d)
+
+    wall = timed(step, args.steps, args.warmup, torch)
+    wall_c = timed(lambda: _C.attention(q, kb, kr, vb, vr, B, H, H, S, S, d), args.steps, 3, torch)
+    per_bin = 2 * W.algorithmic_bytes_per_key(d, residual=False)
+    per_comp = 2 * W.algorithmic_bytes_per_key(d)
+    alg = S * (n_bin * per_bin + n_comp * per_comp)
+    return {
+        "metric": "per-head-mode decode-attn µs/step + achieved HBM GB/s, c3 cache, entropy-median dispatch",
+        "value": round(alg / wall / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4),
+        "us_per_step": round(wall * 1e6, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "c3 cache, per-head modes from entropy >= median (binary) else compensated",
+                   "batch": B, "heads": H, "seq_len": S, "head_dim": d, "binary_heads": n_bin,
+                   "compensated_heads": n_comp, "bytes_per_step": alg},
+        "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_profiles("head_mode_c3_mixed.md", "traffic_bytes_per_step_mixed"),
+                     "kernel": "attention step (binary launch + mixed launch + combine), wall clock"},
+        "full_compensated_us": round(wall_c * 1e6, 1),
+        "step_frac_of_compensated": round(wall / wall_c, 4),
+        "bytes_frac_of_compensated": round(alg / (B * H * S * per_comp), 4),
     }
 
 
@@ -373,6 +435,7 @@ def main():
         fn = {"c2": lambda: bench_c2(args, torch, _C, W),
               "c4": lambda: bench_c4(args, torch, _C, W, bitcache_amd),
               "c5": lambda: bench_c5(args, torch, _C, W),
+              "mixed": lambda: bench_mixed(args, torch, _C, W),
               "prefill": lambda: bench_prefill(args, torch, _C, W)}[args.config]
         print(json.dumps(fn()), flush=True)
         return
@@ -401,7 +464,16 @@ def main():
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
-        print(json.dumps({"probe": "done", "copy_bytes": 1 << 30, "attention_steps": args.steps}))
+        # the fp16 reference kernel and the head entropy on the same workload
+        if not args.no_fp16:
+            for _ in range(args.steps):
+                _C.reference_attention(q, k, v, B, H, H, S, d)
+        for _ in range(args.steps):
+            _C.compute_head_entropy(q, kb, B, H, S, d)
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "done", "copy_bytes": 1 << 30, "attention_steps": args.steps,
+                          "reference_steps": 0 if args.no_fp16 else args.steps,
+                          "entropy_steps": args.steps}))
         return
 
     for _ in range(args.warmup):

@@ -1016,6 +1016,15 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     // one split per group the matrix-core kernel normalises and writes the
     // output itself (no merge launch).
     if (direct_out != nullptr && p.n_splits == 1) a.out = (uint16_t*)direct_out;
+    // per-head modes on the matrix cores: the groups of binary heads only go
+    // to the binary kernel, which reads none of their residual bytes; both
+    // launches cover the grid and each skips the other's groups
+    if (!valu_forced() && mode == MODE_MIXED && bc::mfma_split_ok(head_dim, a.chunk)) {
+        if (!bc::launch_mfma_split(MODE_BINARY, head_dim, p.G, a, grid, st))
+            return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
+        const int rc = bc::check_launch("attention split (mfma, binary heads)");
+        if (rc != BC_OK) return rc;
+    }
     if (!valu_forced() && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st)) {
         if (wrote_out) *wrote_out = a.out != nullptr;
         return bc::check_launch("attention split (mfma)");

@@ -162,9 +162,8 @@ def entropy_dispatch_attention(Q: Tensor, K_bin: Tensor, K_res: Tensor, V_bin: T
 def _capacity(blob: Tensor, per: int) -> int:
     """Vectors a blob was laid out for: its storage's when it is a prefix view
     of a larger allocation, else its own (the operators' rule)."""
-    stor = blob.untyped_storage().nbytes()
-    prefix = blob.storage_offset() == 0 and blob.numel() < stor
-    return (stor if prefix else blob.numel()) // per
+    from bitcache_amd.layout import blob_bytes
+    return blob_bytes(blob) // per
 
 
 def reference_attention(Q: Tensor, K: Tensor, V: Tensor, batch: int, n_heads: int, seq_len: int,

@@ -454,7 +454,10 @@ def test_head_mode_attention(F, B, Hq, Hkv, S, d):
     qt = torch.from_numpy(q).cuda()
     rng = np.random.default_rng(S)
     modes = rng.integers(0, 2, size=(B, Hq)).astype(np.uint8)
-    modes[0, 0], modes[-1, -1] = 0, 1
+    # a query-head group of binary heads only (its workgroups read no
+    # residual bytes) and one of compensated heads only
+    G = Hq // Hkv
+    modes[0, :G], modes[-1, -G:] = 0, 1
     out = to_np(F.head_mode_attention(qt, kb, kr, vb, vr, torch.from_numpy(modes).cuda(), B, Hq, S, d,
                                       n_kv_heads=Hkv)).astype(np.float32)
     n = B * Hkv * S
@@ -471,6 +474,12 @@ def test_head_mode_attention(F, B, Hq, Hkv, S, d):
     comp = F.compensated_attention(qt, kb, kr, vb, vr, B, Hq, S, d, n_kv_heads=Hkv)
     close(to_np(allc).astype(np.float32), to_np(comp).astype(np.float32), rel=1e-3, cos=0.999999,
           what="all heads compensated")
+    # every head binary: no workgroup reads a residual byte; the binary
+    # kernel's output to rounding
+    allb = F.head_mode_attention(qt, kb, kr, vb, vr, torch.zeros_like(ones), B, Hq, S, d, n_kv_heads=Hkv)
+    binr = F.binary_attention(qt, kb, vb, B, Hq, S, d, n_kv_heads=Hkv)
+    close(to_np(allb).astype(np.float32), to_np(binr).astype(np.float32), rel=1e-3, cos=0.999999,
+          what="all heads binary")
 
 
 def test_entropy_dispatch_attention(F):

@@ -236,6 +236,42 @@ def test_reference_layout_conversion(F):
         assert torch.equal(layout.from_reference(layout.to_reference(r, d, True), d, True)[:pr], r[:pr])
 
 
+def test_layout_planes_of_a_bitcache_prefix_view(F):
+    """layout.binary_planes / residual_planes / to_reference on the prefix
+    views the reference's BitCache.attend slices (bitcache/__init__.py:134-139)
+    read the planes of the whole ring blob the view belongs to: the same
+    tensors as on the whole blob, and the slots written so far hold the
+    oracle's online-encode bytes of the appended vectors."""
+    from bitcache_amd import BitCache, layout
+    say("case layout prefix view")
+    B, H, d, max_seq, steps = 2, 2, 128, 40, 13
+    c = BitCache(B, H, d, max_seq)
+    rng = np.random.default_rng(41)
+    ks = []
+    for _ in range(steps):
+        k = (rng.standard_normal((B, H, d)) * 0.3).astype(np.float16)
+        c.append(torch.from_numpy(k).cuda(), torch.from_numpy(k).cuda())
+        ks.append(k)
+    n = B * H * max_seq
+    vb = c._k_bin[:B * H * steps * 36]
+    vr = c._k_res[:B * H * steps * 130]
+    assert vb.numel() < c._k_bin.numel()
+    for got, want in zip(layout.binary_planes(vb, d), layout.binary_planes(c._k_bin, d)):
+        assert got.shape[0] == n and torch.equal(got, want)
+    for got, want in zip(layout.residual_planes(vr, d), layout.residual_planes(c._k_res, d)):
+        assert got.shape[0] == n and torch.equal(got, want)
+    assert torch.equal(layout.to_reference(vb, d, False), layout.to_reference(c._k_bin, d, False))
+    signs, scale = layout.binary_planes(vb, d)
+    codes, rscale = layout.residual_planes(vr, d)
+    x = np.stack(ks, axis=2).reshape(B * H * steps, d)          # row (b, h), slot s
+    eb, er = O.online_encode(x)
+    rows = (np.arange(B * H)[:, None] * max_seq + np.arange(steps)[None]).reshape(-1)
+    assert np.array_equal(to_np(signs)[rows].view(np.uint32), eb.words)
+    assert np.array_equal(to_np(scale)[rows].view(np.uint16), eb.scale.view(np.uint16))
+    assert np.array_equal(O.unpack_nibbles(to_np(codes)[rows]), er.codes)
+    assert np.array_equal(to_np(rscale)[rows].view(np.uint16), er.scale.view(np.uint16))
+
+
 def test_encode_prefill_scale_property(F):
     """c3-sized prefill slice: fused fp16-scale encode == two-step encode bytes
     on 2M vectors, and a random sample of vectors matches the oracle."""
