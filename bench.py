@@ -382,14 +382,32 @@ def bench_prefill(args, torch, _C, W):
     floor_ms = event_ms(lambda: (_C.encode_traffic_probe(kf, pb, pr), _C.encode_traffic_probe(vf, pb, pr)),
                         steps, torch) / 2
     del pb, pr
+    # the device's mixed read/write ceiling for this traffic shape: 3 bytes
+    # read per byte written (the encoder: 256 B in, 84 B out per vector) with
+    # whole-line stores, plain and nontemporal, over the same 4.29 GB of reads
+    mix_w = (n * 2 * d // 3) // 4096 * 4096
+    mdst = torch.empty(mix_w, dtype=torch.uint8, device=q.device)
+    kbytes = kf.view(torch.uint8).view(-1)
+    mix = {}
+    for nt in (False, True):
+        _C.mix_probe(kbytes, mdst, nt)
+        ms = event_ms(lambda: _C.mix_probe(kbytes, mdst, nt), steps, torch)
+        mix[nt] = (4 * mix_w) / (ms * 1e-3) / 1e9
+    del mdst, kbytes
     kb, _ = _C.encode_fused(kf, False)
     del k, v, kf, vf
     torch.cuda.synchronize()
     ent_ms = event_ms(lambda: _C.compute_head_entropy(q, kb, B, H, S, d), steps, torch)
+    # one read of the entropy pass's bytes (sign rows + scales) in one launch
+    ent_bytes = n * (d // 8 + 2)
+    rbuf = torch.ones(ent_bytes // 16 * 16, dtype=torch.uint8, device=q.device)
+    _C.read_probe(rbuf)
+    ent_rd_ms = event_ms(lambda: _C.read_probe(rbuf), steps, torch)
+    del rbuf
     per_vec = 2 * d + (d // 8 + 2) + (d // 2 + 2)      # fp16 in; signs, scale, codes, absmax out
     alg = n * per_vec
     gbs = alg / (enc_ms * 1e-3) / 1e9
-    ent_bytes = n * (d // 8 + 2)
+    mix_best = max(mix.values())
     return {
         "metric": "prefill encode µs per K or V tensor + achieved GB/s, c3 cache (16.8M vectors, d=128)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": 0,
@@ -406,8 +424,16 @@ def bench_prefill(args, torch, _C, W):
         "traffic_floor_us": round(floor_ms * 1e3, 1),
         "traffic_floor_gbps": round(alg / (floor_ms * 1e-3) / 1e9, 1),
         "frac_of_traffic_floor": round(floor_ms / enc_ms, 4),
+        "mix_ceiling": {"gbps": round(mix_best, 1), "plain_store_gbps": round(mix[False], 1),
+                        "nt_store_gbps": round(mix[True], 1),
+                        "encoder_frac_of_ceiling": round(gbs / mix_best, 4),
+                        "what": "bc_mix_probe: 3 B read per B written, 16-B loads, whole-line 16-B stores"},
         "entropy_us": round(ent_ms * 1e3, 1),
         "entropy_gbps": round(ent_bytes / (ent_ms * 1e-3) / 1e9, 1),
+        "entropy_read_ceiling": {"us": round(ent_rd_ms * 1e3, 1),
+                                 "gbps": round(ent_bytes / (ent_rd_ms * 1e-3) / 1e9, 1),
+                                 "entropy_frac_of_ceiling": round(ent_rd_ms / ent_ms, 4),
+                                 "what": "one bc_read_probe read of the pass's 302 MB"},
     }
 
 

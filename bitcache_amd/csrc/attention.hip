@@ -684,17 +684,22 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
 // src/adaptive_precision.cu:13-130.  Tree-order scale_q (thread t of 128
 // holds |q_t| + |q_{t+128}|, tree s = 64..1), scores without 1/sqrt(d),
 // H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread,
-// merged over the block.  One block of kEntropyThreads per (b, h).
+// merged over the block.  A block of T threads takes key chunk blockIdx.x of
+// (b, h) = blockIdx.y: with one chunk per head it writes H (T = 1024, the
+// entry points without a workspace); with several it writes its (M, Z, W) to
+// the workspace and entropy_merge_kernel finishes each head (T = 256, about
+// eight blocks per CU: one block per head cannot draw a CU's share of HBM).
 constexpr int kEntropyThreads = 1024;
-template <int D>
-__global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t* q, BinPlanes kb,
-                                                                  float* out, int Hq, int Hkv,
-                                                                  int S, int kv_stride) {
-    constexpr int NW = kEntropyThreads / 64;
+constexpr int kEntPartThreads = 256;
+template <int D, int T>
+__global__ __launch_bounds__(T) void entropy_kernel(const uint16_t* q, BinPlanes kb, float* out,
+                                                    float* ws, int Hq, int Hkv, int S,
+                                                    int kv_stride, int chunk) {
+    constexpr int NW = T / 64;
     __shared__ float part[128];
     __shared__ uint32_t qs[D / 32];
     __shared__ float sm[NW], sz[NW], sw[NW];
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.y, c = blockIdx.x;
     const uint16_t* qb = q + (int64_t)bh * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 128) {
@@ -716,23 +721,24 @@ __global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t
     // query head h of batch b reads kv head h / (Hq / Hkv) of that batch
     const int b = bh / Hq, kvh = (bh % Hq) / (Hq / Hkv);
     const int64_t base = ((int64_t)b * Hkv + kvh) * kv_stride;
-    // online (M, Z, W) per thread over keys tid, tid + T, ...; four keys'
+    const int k0 = c * chunk, k1 = min(S, k0 + chunk);
+    // online (M, Z, W) per thread over keys k0 + tid, + T, ...; four keys'
     // loads in flight per thread
     constexpr int U = 4;
     float M = -1e30f, Z = 0.0f, W = 0.0f;
-    for (int s0 = tid; s0 < S; s0 += U * kEntropyThreads) {
+    for (int s0 = k0 + tid; s0 < k1; s0 += U * T) {
         SignWords<D> ks[U];
         float skv[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int s = s0 + u * kEntropyThreads;
-            const int64_t i = base + (s < S ? s : s0);
+            const int s = s0 + u * T;
+            const int64_t i = base + (s < k1 ? s : s0);
             ks[u] = load_signs<D, true>(kb.signs + i * (D / 8));
             skv[u] = h2f(kb.scales[i]);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (s0 + u * kEntropyThreads >= S) break;
+            if (s0 + u * T >= k1) break;
             int pc = 0;
 #pragma unroll
             for (int w = 0; w < D / 32; w++) pc += __builtin_popcount(~(qs[w] ^ ks[u].w[w]));
@@ -773,8 +779,31 @@ __global__ __launch_bounds__(kEntropyThreads) void entropy_kernel(const uint16_t
             z += sz[i] * f;
             w += sw[i] * f;
         }
-        out[bh] = (logf(z) + gm) - w / fmaxf(z, 1e-12f);
+        if (ws != nullptr) {
+            float* p = ws + ((int64_t)bh * gridDim.x + c) * 3;
+            p[0] = gm;
+            p[1] = z;
+            p[2] = w;
+        } else {
+            out[bh] = (logf(z) + gm) - w / fmaxf(z, 1e-12f);
+        }
     }
+}
+
+// H per (b, h) from its nchunk (M, Z, W) partials (one thread per head)
+__global__ void entropy_merge_kernel(const float* ws, float* out, int n, int nchunk) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float* p = ws + (int64_t)i * nchunk * 3;
+    float gm = -1e30f;
+    for (int c = 0; c < nchunk; c++) gm = fmaxf(gm, p[3 * c]);
+    float z = 0.0f, w = 0.0f;
+    for (int c = 0; c < nchunk; c++) {
+        const float f = expf(p[3 * c] - gm);
+        z += p[3 * c + 1] * f;
+        w += p[3 * c + 2] * f;
+    }
+    out[i] = (logf(z) + gm) - w / fmaxf(z, 1e-12f);
 }
 
 __global__ void select_kernel(const float* e, uint8_t* modes, int n, float thr) {
@@ -1288,25 +1317,74 @@ extern "C" int bc_binary_scores(const void* q, const void* k_bin, float* scores,
     return bc::check_launch("binary scores");
 }
 
+// key chunks per (b, query head) of the entropy pass: about eight 256-thread
+// blocks per CU over all heads, at least 4096 keys per chunk; one chunk means
+// the single-block kernel (no workspace)
+static int entropy_chunks(int batch, int hq, int S) {
+    const int64_t heads = (int64_t)batch * hq;
+    if (heads <= 0 || S <= 0) return 1;
+    int64_t n = (8LL * bc::device_cu_count() + heads - 1) / heads;
+    const int64_t most = ((int64_t)S + 4095) / 4096;
+    if (n > most) n = most;
+    return n < 1 ? 1 : (int)n;
+}
+
+static size_t entropy_ws_bytes(int batch, int hq, int S) {
+    const int n = entropy_chunks(batch, hq, S);
+    return n <= 1 ? 0 : (size_t)batch * hq * n * 3 * sizeof(float);
+}
+
 template <int D>
-static void launch_entropy(const void* q, BinPlanes kb, float* out, int batch, int hq, int hkv,
-                           int S, int stride, hipStream_t st) {
-    hipLaunchKernelGGL((entropy_kernel<D>), dim3(batch * hq), dim3(kEntropyThreads), 0, st,
-                       (const uint16_t*)q, kb, out, hq, hkv, S, stride);
+static void launch_entropy(const void* q, BinPlanes kb, float* out, float* ws, int batch, int hq,
+                           int hkv, int S, int stride, hipStream_t st) {
+    const int n = ws != nullptr ? entropy_chunks(batch, hq, S) : 1;
+    if (n <= 1) {
+        hipLaunchKernelGGL((entropy_kernel<D, kEntropyThreads>), dim3(1, batch * hq),
+                           dim3(kEntropyThreads), 0, st, (const uint16_t*)q, kb, out,
+                           (float*)nullptr, hq, hkv, S, stride, S);
+        return;
+    }
+    const int chunk = (S + n - 1) / n;
+    hipLaunchKernelGGL((entropy_kernel<D, kEntPartThreads>), dim3(n, batch * hq),
+                       dim3(kEntPartThreads), 0, st, (const uint16_t*)q, kb, out, ws, hq, hkv, S,
+                       stride, chunk);
+    const int heads = batch * hq;
+    hipLaunchKernelGGL(entropy_merge_kernel, dim3((heads + 255) / 256), dim3(256), 0, st,
+                       (const float*)ws, out, heads, n);
+}
+
+extern "C" int bc_entropy_workspace_size(int batch, int n_heads, int seq_len, size_t* bytes) {
+    BC_REQUIRE(batch >= 0 && n_heads >= 0 && seq_len >= 0, BC_ERR_INVALID_ARGUMENT,
+               "invalid dims batch=%d n_heads=%d seq_len=%d", batch, n_heads, seq_len);
+    BC_REQUIRE(bytes != nullptr, BC_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = entropy_ws_bytes(batch, n_heads, seq_len);
+    return BC_OK;
+}
+
+extern "C" int bc_compute_head_entropy_ws(const void* q, const void* k_bin, float* entropy,
+                                          int batch, int n_heads, int n_kv_heads, int seq_len,
+                                          int kv_stride, int head_dim, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
+    if (v != BC_OK) return v;
+    if ((int64_t)batch * n_heads == 0) return BC_OK;
+    BC_REQUIRE(q && k_bin && entropy, BC_ERR_INVALID_ARGUMENT, "null pointer");
+    const size_t need = entropy_ws_bytes(batch, n_heads, seq_len);
+    BC_REQUIRE(workspace == nullptr || workspace_bytes >= need, BC_ERR_WORKSPACE,
+               "workspace of %zu bytes required, got %zu", need, workspace_bytes);
+    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
+    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
+    float* ws = need > 0 ? (float*)workspace : nullptr;
+    BC_DISPATCH_D(head_dim, launch_entropy, q, kb, entropy, ws, batch, n_heads, n_kv_heads,
+                  seq_len, kv_stride, (hipStream_t)stream);
+    return bc::check_launch("entropy");
 }
 
 extern "C" int bc_compute_head_entropy_gqa(const void* q, const void* k_bin, float* entropy,
                                            int batch, int n_heads, int n_kv_heads, int seq_len,
                                            int kv_stride, int head_dim, void* stream) {
-    int v = validate_heads(batch, n_heads, n_kv_heads, seq_len, kv_stride, head_dim);
-    if (v != BC_OK) return v;
-    if ((int64_t)batch * n_heads == 0) return BC_OK;
-    BC_REQUIRE(q && k_bin && entropy, BC_ERR_INVALID_ARGUMENT, "null pointer");
-    const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
-    BinPlanes kb = bin_planes(k_bin, cap, head_dim);
-    BC_DISPATCH_D(head_dim, launch_entropy, q, kb, entropy, batch, n_heads, n_kv_heads, seq_len,
-                  kv_stride, (hipStream_t)stream);
-    return bc::check_launch("entropy");
+    return bc_compute_head_entropy_ws(q, k_bin, entropy, batch, n_heads, n_kv_heads, seq_len,
+                                      kv_stride, head_dim, nullptr, 0, stream);
 }
 
 extern "C" int bc_compute_head_entropy(const void* q, const void* k_bin, float* entropy,

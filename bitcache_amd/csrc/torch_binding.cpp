@@ -166,6 +166,18 @@ void encode_traffic_probe(torch::Tensor src, torch::Tensor bin, torch::Tensor re
 // The device's streaming-read ceiling: reads src's bytes once (measurement
 // aid); returns the output words, of which the first 4 per workgroup (four
 // workgroups per CU, at most one per 16 bytes) hold the per-wave XORs
+// One mixed stream: reads 3 * dst's bytes of src, writes dst (bc_mix_probe).
+void mix_probe(torch::Tensor src, torch::Tensor dst, bool nt_store) {
+    TORCH_CHECK(src.is_cuda() && src.is_contiguous() && dst.is_cuda() && dst.is_contiguous(),
+                "src and dst must be contiguous device tensors");
+    check_same_device(src, dst, "dst");
+    const int64_t nw = dst.numel() * dst.element_size();
+    TORCH_CHECK(src.numel() * src.element_size() >= 3 * nw, "src must hold 3x dst's bytes");
+    c10::DeviceGuard guard(src.device());
+    check_status(bc_mix_probe(src.data_ptr(), dst.data_ptr(), nw, nt_store ? 1 : 0, stream_of(src)),
+                 "mix_probe");
+}
+
 torch::Tensor read_probe(torch::Tensor src) {
     TORCH_CHECK(src.is_cuda() && src.is_contiguous(), "src must be a contiguous device tensor");
     const int64_t n = src.numel() * src.element_size();
@@ -509,7 +521,7 @@ std::tuple<torch::Tensor, torch::Tensor> binary_scores(torch::Tensor Q, torch::T
     return {scores, pcs};
 }
 
-// GQA / ring-stride form (bc_compute_head_entropy_gqa).
+// GQA / ring-stride form (bc_compute_head_entropy_ws).
 torch::Tensor head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t batch, int64_t n_heads,
                            int64_t n_kv_heads, int64_t seq_len, int64_t kv_stride,
                            int64_t head_dim) {
@@ -519,9 +531,17 @@ torch::Tensor head_entropy(torch::Tensor Q, torch::Tensor K_bin, int64_t batch, 
     void* kb = blob_exact(K_bin, batch * n_kv_heads * kv_stride, bc_sizeof_binary_vec(), "K_bin");
     c10::DeviceGuard guard(Q.device());
     auto ent = torch::empty({batch, n_heads}, Q.options().dtype(torch::kFloat32));
-    check_status(bc_compute_head_entropy_gqa(Q.data_ptr(), kb, ent.data_ptr<float>(), (int)batch,
-                                             (int)n_heads, (int)n_kv_heads, (int)seq_len,
-                                             (int)kv_stride, (int)head_dim, stream_of(Q)),
+    // the key-split pass (several blocks per head) with a workspace from the
+    // caching allocator; the same result as the single-block entry points
+    size_t ws_bytes = 0;
+    check_status(bc_entropy_workspace_size((int)batch, (int)n_heads, (int)seq_len, &ws_bytes),
+                 "entropy_workspace_size");
+    auto ws = workspace_for(Q, ws_bytes);
+    check_status(bc_compute_head_entropy_ws(Q.data_ptr(), kb, ent.data_ptr<float>(), (int)batch,
+                                            (int)n_heads, (int)n_kv_heads, (int)seq_len,
+                                            (int)kv_stride, (int)head_dim,
+                                            ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
+                                            stream_of(Q)),
                  "compute_head_entropy");
     return ent;
 }
@@ -615,6 +635,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("encode_traffic_probe", &encode_traffic_probe,
           "encode_fused's loads and stores without its arithmetic (memory floor)");
     m.def("read_probe", &read_probe, "One streaming read of a tensor's bytes (the read ceiling)");
+    m.def("mix_probe", &mix_probe, "A 3:1 read/write stream (the encoders' mixed-traffic ceiling)",
+          py::arg("src"), py::arg("dst"), py::arg("nt_store") = false);
     m.def("online_encode_kv", &online_encode_kv, "K and V token encode in one launch");
     m.def("encode_into_cache", &encode_into_cache, "Bulk prefill into ring caches");
     m.def("encode_into_cache_bshd", &encode_into_cache_bshd,

@@ -129,6 +129,14 @@ int bc_encode_traffic_probe(const void* src, void* binary_blob, void* residual_b
  * uint32).  Time it to read the attention kernels' bandwidth against what
  * the memory system delivers.  No counterpart in the reference; a
  * measurement aid for benchmarks. */
+/* The device's mixed read/write ceiling for the encoders' traffic shape:
+ * reads 3 * n_write_bytes from src (nontemporal 16-byte loads, three coalesced
+ * KiB per wave) and writes n_write_bytes to dst (16 bytes per lane, whole
+ * cache lines; nt_store != 0: nontemporal stores), four workgroups per CU.
+ * n_write_bytes a multiple of 4096, src and dst 16-byte aligned.  No
+ * counterpart in the reference; a measurement aid for benchmarks. */
+int bc_mix_probe(const void* src, void* dst, int64_t n_write_bytes, int nt_store, void* stream);
+
 #define BC_READ_PROBE_MAX_WGS 4096
 #define BC_READ_PROBE_OUT_WORDS (4 * BC_READ_PROBE_MAX_WGS)
 int bc_read_probe(const void* src, int64_t n_bytes, void* out, void* stream);
@@ -252,6 +260,18 @@ int bc_compute_head_entropy(const void* q, const void* k_bin, float* entropy, in
 int bc_compute_head_entropy_gqa(const void* q, const void* k_bin, float* entropy, int batch,
                                 int n_heads, int n_kv_heads, int seq_len, int kv_stride,
                                 int head_dim, void* stream);
+
+/* bc_compute_head_entropy_gqa over several blocks per head: each block takes a
+ * key chunk and leaves its (max, sum e, sum e*s) in the workspace, and a second
+ * launch merges them (the single-block entry points keep one block per head,
+ * which cannot draw a CU's share of HBM bandwidth).  Workspace bytes from
+ * bc_entropy_workspace_size (0: the shape runs one block per head; a NULL
+ * workspace selects the single-block kernel).  Same entropies to fp32
+ * rounding.  No counterpart in the reference. */
+int bc_entropy_workspace_size(int batch, int n_heads, int seq_len, size_t* bytes);
+int bc_compute_head_entropy_ws(const void* q, const void* k_bin, float* entropy, int batch,
+                               int n_heads, int n_kv_heads, int seq_len, int kv_stride,
+                               int head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
 /* mode[i] = entropy[i] >= threshold ? 0 (binary) : 1 (compensated).
  * Replaces launch_adaptive_select (src/adaptive_precision.cu:171-186). */

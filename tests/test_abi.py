@@ -93,6 +93,13 @@ def test_encode_argument_errors(lib, no_gpu):
     assert t(fake, fake, fake, -1, 128, None) == BC_ERR_INVALID_ARGUMENT
     assert t(fake, None, fake, 10, 128, None) == BC_ERR_INVALID_ARGUMENT
     assert t(None, None, None, 0, 128, None) == BC_OK
+    m = lib.bc_mix_probe
+    m.argtypes = [P, P, ctypes.c_int64, ctypes.c_int, P]
+    assert m(fake, fake, 4096 + 16, 0, None) == BC_ERR_INVALID_ARGUMENT   # not whole 4 KiB blocks
+    assert m(fake, fake, 24, 0, None) == BC_ERR_INVALID_ARGUMENT
+    assert m(fake, P(0x1008), 4096, 0, None) == BC_ERR_INVALID_ARGUMENT  # unaligned
+    assert m(None, fake, 4096, 0, None) == BC_ERR_INVALID_ARGUMENT
+    assert m(None, None, 0, 0, None) == BC_OK
     r = lib.bc_read_probe
     r.argtypes = [P, ctypes.c_int64, P, P]
     assert r(fake, 24, fake, None) == BC_ERR_INVALID_ARGUMENT        # not a multiple of 16
@@ -149,6 +156,15 @@ def test_attention_argument_errors(lib, no_gpu):
     na.argtypes = [P] * 6 + [ctypes.c_int] * 6 + [P]
     assert na(*[fake] * 6, 4096, 64, 8, 1 << 20, 1 << 20, 128, None) == BC_ERR_WORKSPACE
     assert b"allocation-free" in lib.bc_last_error()
+    ew = lib.bc_entropy_workspace_size
+    ew.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(size_t)]
+    assert ew(1, 4, 100, ctypes.byref(n)) == BC_OK and n.value == 0        # one block per head
+    assert ew(8, 32, 65536, ctypes.byref(n)) == BC_OK and n.value > 0      # key chunks
+    assert ew(-1, 4, 100, ctypes.byref(n)) == BC_ERR_INVALID_ARGUMENT
+    es = lib.bc_compute_head_entropy_ws
+    es.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [P, size_t, P]
+    assert es(fake, fake, fake, 8, 32, 32, 65536, 65536, 128, fake, 1, None) == BC_ERR_WORKSPACE
+    assert es(fake, fake, fake, 1, 6, 4, 100, 100, 128, None, 0, None) == BC_ERR_INVALID_ARGUMENT
     e = lib.bc_compute_head_entropy_gqa
     e.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [P]
     assert e(fake, fake, fake, 1, 6, 4, 100, 100, 128, None) == BC_ERR_INVALID_ARGUMENT  # 6 % 4

@@ -316,6 +316,28 @@ def test_read_probe_reads_every_word_once(n_bytes):
     assert got == want
 
 
+@pytest.mark.parametrize("n_write,nt", [(4096, False), (4096 * 1021, True), (4096 * 9000, False)])
+def test_mix_probe_writes_each_word_once(n_write, nt):
+    """The mixed read/write probe: output word j (16 bytes) is the XOR of the
+    three input words 768 * (j // 256) + 256 r + j % 256, r = 0..2, so every
+    input is read once and every output written once; a guard region past
+    dst stays untouched."""
+    from bitcache_amd import _C
+    say(f"case mix probe {n_write} nt={nt}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(n_write)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (3 * n_write // 4,), dtype=torch.int32, device="cuda",
+                        generator=g)
+    buf = torch.full((n_write // 4 + 1024,), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+    dst = buf[: n_write // 4]
+    _C.mix_probe(src, dst, nt)
+    torch.cuda.synchronize()
+    w = src.cpu().numpy().reshape(-1, 3, 256, 4)             # [block, r, word, 4 x u32]
+    want = (w[:, 0] ^ w[:, 1] ^ w[:, 2]).reshape(-1)
+    assert np.array_equal(dst.cpu().numpy(), want)
+    assert bool((buf[n_write // 4:] == 0x5A5A5A5A).all())
+
+
 @pytest.mark.parametrize("d,n", [(64, 5000), (128, 3001), (256, 777)])
 def test_traffic_probe_stays_in_its_blobs(d, n):
     """The encoder's traffic probe (same loads and stores, no arithmetic)
