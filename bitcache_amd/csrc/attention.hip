@@ -684,8 +684,8 @@ __global__ __launch_bounds__(256) void scores_kernel(const uint16_t* q, BinPlane
 // src/adaptive_precision.cu:13-130.  Tree-order scale_q (thread t of 128
 // holds |q_t| + |q_{t+128}|, tree s = 64..1), scores without 1/sqrt(d),
 // H = (log Z + M) - W / max(Z, 1e-12) with an online (M, Z, W) per thread,
-// merged over the block.  A block of T threads takes key chunk blockIdx.x of
-// (b, h) = blockIdx.y: with one chunk per head it writes H (T = 1024, the
+// merged over the block.  A block of T threads takes key chunk blockIdx.y of
+// (b, h) = blockIdx.x: with one chunk per head it writes H (T = 1024, the
 // entry points without a workspace); with several it writes its (M, Z, W) to
 // the workspace and entropy_merge_kernel finishes each head (T = 256, about
 // eight blocks per CU: one block per head cannot draw a CU's share of HBM).
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(T) void entropy_kernel(const uint16_t* q, BinPlanes
     __shared__ float part[128];
     __shared__ uint32_t qs[D / 32];
     __shared__ float sm[NW], sz[NW], sw[NW];
-    const int bh = blockIdx.y, c = blockIdx.x;
+    const int bh = blockIdx.x, c = blockIdx.y;
     const uint16_t* qb = q + (int64_t)bh * D;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 128) {
@@ -780,7 +780,7 @@ __global__ __launch_bounds__(T) void entropy_kernel(const uint16_t* q, BinPlanes
             w += sw[i] * f;
         }
         if (ws != nullptr) {
-            float* p = ws + ((int64_t)bh * gridDim.x + c) * 3;
+            float* p = ws + ((int64_t)bh * gridDim.y + c) * 3;
             p[0] = gm;
             p[1] = z;
             p[2] = w;
@@ -1339,13 +1339,13 @@ static void launch_entropy(const void* q, BinPlanes kb, float* out, float* ws, i
                            int hkv, int S, int stride, hipStream_t st) {
     const int n = ws != nullptr ? entropy_chunks(batch, hq, S) : 1;
     if (n <= 1) {
-        hipLaunchKernelGGL((entropy_kernel<D, kEntropyThreads>), dim3(1, batch * hq),
+        hipLaunchKernelGGL((entropy_kernel<D, kEntropyThreads>), dim3(batch * hq, 1),
                            dim3(kEntropyThreads), 0, st, (const uint16_t*)q, kb, out,
                            (float*)nullptr, hq, hkv, S, stride, S);
         return;
     }
     const int chunk = (S + n - 1) / n;
-    hipLaunchKernelGGL((entropy_kernel<D, kEntPartThreads>), dim3(n, batch * hq),
+    hipLaunchKernelGGL((entropy_kernel<D, kEntPartThreads>), dim3(batch * hq, n),
                        dim3(kEntPartThreads), 0, st, (const uint16_t*)q, kb, out, ws, hq, hkv, S,
                        stride, chunk);
     const int heads = batch * hq;

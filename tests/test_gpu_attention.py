@@ -230,34 +230,37 @@ def test_entropy_vs_oracle(F):
     assert np.array_equal(modes, (ent < np.median(ent)).astype(np.uint8))
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,S,d", [(1, 4, 4, 40000, 128), (2, 8, 2, 30001, 64),
-                                          (1, 2, 2, 17000, 256), (1, 4, 1, 9000, 96)])
-def test_entropy_key_split_vs_oracle_and_single_block(F, B, Hq, Hkv, S, d):
+@pytest.mark.parametrize("B,Hq,Hkv,S,stride,d", [(1, 4, 4, 40000, 40000, 128), (2, 8, 2, 30001, 30001, 64),
+                                                 (1, 2, 2, 17000, 17000, 256), (1, 4, 1, 9000, 9000, 96),
+                                                 (2, 4, 2, 20000, 23456, 128)])
+def test_entropy_key_split_vs_oracle_and_single_block(F, B, Hq, Hkv, S, stride, d):
     """The key-split entropy pass (several blocks per head, partials merged by a
     second launch; what the operator module runs when a head's keys span more
     than one chunk) against the oracle, and against the single-block kernel of
-    the reference-signature C entry point to fp32 rounding."""
+    the reference-signature C entry point to fp32 rounding; GQA groups and a
+    ring stride past the filled keys included."""
     import ctypes
     import os
-    say(f"case entropy split B={B} Hq={Hq} Hkv={Hkv} S={S} d={d}")
-    q, k, _ = make(B, Hq, Hkv, S, d, seed=S % 1000, scale=0.3)
+    say(f"case entropy split B={B} Hq={Hq} Hkv={Hkv} S={S} stride={stride} d={d}")
+    q, k, _ = make(B, Hq, Hkv, stride, d, seed=S % 1000, scale=0.3)
     kb = F.encode(torch.from_numpy(k.reshape(-1, d)).cuda())
     qt = torch.from_numpy(q).cuda()
+    k = np.ascontiguousarray(k[:, :, :S])
     L = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
                                  "bitcache_amd", "libbitcache_hip.so"))
     n = ctypes.c_size_t(0)
     L.bc_entropy_workspace_size.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_size_t)]
     assert L.bc_entropy_workspace_size(B, Hq, S, ctypes.byref(n)) == 0
     assert n.value > 0, "this shape should take the key-split pass"
-    ent = to_np(F.compute_head_entropy(qt, kb, B, Hq, S, d, n_kv_heads=Hkv))
-    Kb = bin_from_blob(kb, B * Hkv * S, d)
+    ent = to_np(F.compute_head_entropy(qt, kb, B, Hq, S, d, n_kv_heads=Hkv, kv_stride=stride))
+    Kb = O.binary_encode(k.reshape(-1, d))
     ref = O.head_entropy(q, Kb, B, Hq, S, n_kv_heads=Hkv)
     np.testing.assert_allclose(ent, ref, rtol=2e-4, atol=2e-4)
     one = torch.empty((B, Hq), dtype=torch.float32, device="cuda")
     P = ctypes.c_void_p
     L.bc_compute_head_entropy_gqa.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [P]
     assert L.bc_compute_head_entropy_gqa(P(qt.data_ptr()), P(kb.data_ptr()), P(one.data_ptr()), B, Hq,
-                                         Hkv, S, S, d, P(torch.cuda.current_stream().cuda_stream)) == 0
+                                         Hkv, S, stride, d, P(torch.cuda.current_stream().cuda_stream)) == 0
     torch.cuda.synchronize()
     np.testing.assert_allclose(ent, to_np(one), rtol=1e-5, atol=1e-5)
 
