@@ -127,6 +127,15 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const int kvh = bkv % a.Hkv;
     const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
     const int bhq0 = b * a.Hq + hq0;
+    // per-head modes as two launches (as the matrix-core kernel): the binary
+    // kernel takes the groups of binary heads only, the mixed kernel the rest
+    if constexpr (MODE == MODE_BINARY || MODE == MODE_MIXED) {
+        if (a.head_mode != nullptr) {
+            bool any_res = false;
+            for (int g = 0; g < G; g++) any_res |= a.head_mode[bhq0 + g] != 0;
+            if (MODE == MODE_BINARY ? any_res : !any_res) return;
+        }
+    }
 
     prep_queries<D, G>(a.q + (int64_t)bhq0 * D, qp, qf);
 
@@ -1061,6 +1070,11 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     a.out = nullptr;
     // (the VALU kernel does not append; the append entry point checks first)
     BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
+    if (mode == MODE_MIXED) {
+        BC_DISPATCH_D(head_dim, launch_split_g, MODE_BINARY, p.G, a, grid, st);
+        const int rc = bc::check_launch("attention split (binary heads)");
+        if (rc != BC_OK) return rc;
+    }
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }
