@@ -166,6 +166,16 @@ void encode_traffic_probe(torch::Tensor src, torch::Tensor bin, torch::Tensor re
 // The device's streaming-read ceiling: reads src's bytes once (measurement
 // aid); returns the output words, of which the first 4 per workgroup (four
 // workgroups per CU, at most one per 16 bytes) hold the per-wave XORs
+torch::Tensor read_probe(torch::Tensor src) {
+    TORCH_CHECK(src.is_cuda() && src.is_contiguous(), "src must be a contiguous device tensor");
+    const int64_t n = src.numel() * src.element_size();
+    TORCH_CHECK(n % 16 == 0, "src must hold a multiple of 16 bytes");
+    c10::DeviceGuard guard(src.device());
+    auto out = torch::empty({BC_READ_PROBE_OUT_WORDS}, src.options().dtype(torch::kInt32));
+    check_status(bc_read_probe(src.data_ptr(), n, out.data_ptr(), stream_of(src)), "read_probe");
+    return out;
+}
+
 // One mixed stream: reads 3 * dst's bytes of src, writes dst (bc_mix_probe).
 void mix_probe(torch::Tensor src, torch::Tensor dst, bool nt_store) {
     TORCH_CHECK(src.is_cuda() && src.is_contiguous() && dst.is_cuda() && dst.is_contiguous(),
@@ -176,16 +186,6 @@ void mix_probe(torch::Tensor src, torch::Tensor dst, bool nt_store) {
     c10::DeviceGuard guard(src.device());
     check_status(bc_mix_probe(src.data_ptr(), dst.data_ptr(), nw, nt_store ? 1 : 0, stream_of(src)),
                  "mix_probe");
-}
-
-torch::Tensor read_probe(torch::Tensor src) {
-    TORCH_CHECK(src.is_cuda() && src.is_contiguous(), "src must be a contiguous device tensor");
-    const int64_t n = src.numel() * src.element_size();
-    TORCH_CHECK(n % 16 == 0, "src must hold a multiple of 16 bytes");
-    c10::DeviceGuard guard(src.device());
-    auto out = torch::empty({BC_READ_PROBE_OUT_WORDS}, src.options().dtype(torch::kInt32));
-    check_status(bc_read_probe(src.data_ptr(), n, out.data_ptr(), stream_of(src)), "read_probe");
-    return out;
 }
 
 void check_kv_token(const torch::Tensor& kv, int64_t batch, int64_t n_heads, int64_t d) {
