@@ -120,22 +120,20 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 
     const int split = blockIdx.x;
     const int nqg = (a.Hq / a.Hkv) / G;
-    const int y = blockIdx.y;
+    // per-head modes: this launch's query-head groups come from its list
+    int y = blockIdx.y;
+    if constexpr (MODE == MODE_BINARY || MODE == MODE_MIXED) {
+        if (a.group_list != nullptr) {
+            if (y >= *a.group_count) return;
+            y = a.group_list[y];
+        }
+    }
     const int qg = y % nqg;
     const int bkv = y / nqg;  // b * Hkv + kvh
     const int b = bkv / a.Hkv;
     const int kvh = bkv % a.Hkv;
     const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
     const int bhq0 = b * a.Hq + hq0;
-    // per-head modes as two launches (as the matrix-core kernel): the binary
-    // kernel takes the groups of binary heads only, the mixed kernel the rest
-    if constexpr (MODE == MODE_BINARY || MODE == MODE_MIXED) {
-        if (a.head_mode != nullptr) {
-            bool any_res = false;
-            for (int g = 0; g < G; g++) any_res |= a.head_mode[bhq0 + g] != 0;
-            if (MODE == MODE_BINARY ? any_res : !any_res) return;
-        }
-    }
 
     prep_queries<D, G>(a.q + (int64_t)bhq0 * D, qp, qf);
 
@@ -815,6 +813,56 @@ __global__ void entropy_merge_kernel(const float* ws, float* out, int n, int nch
     out[i] = (logf(z) + gm) - w / fmaxf(z, 1e-12f);
 }
 
+// Query-head groups of per-head modes, compacted in order: group y (heads
+// b*Hq + hq0 .. + G - 1 of grid row y, as the attention kernels map it) goes
+// to the binary list when all its heads have mode 0, else to the mixed list.
+// One block; lists[0], lists[1] = the counts, the lists from word 64 on.
+constexpr int kListThreads = 1024;
+constexpr size_t kListHeader = 256;   // bytes before the lists (the two counts)
+__global__ __launch_bounds__(kListThreads) void mode_groups_kernel(const uint8_t* head_mode,
+                                                                   int32_t* lists, int groups,
+                                                                   int nqg, int Hq, int Hkv,
+                                                                   int G) {
+    __shared__ int wb[kListThreads / 64], wm_[kListThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int32_t* bin_list = lists + kListHeader / sizeof(int32_t);
+    int32_t* mix_list = bin_list + groups;
+    int nb = 0, nm = 0;   // entries written so far (uniform)
+    for (int y0 = 0; y0 < groups; y0 += kListThreads) {
+        const int y = y0 + tid;
+        bool live = y < groups, res = false;
+        if (live) {
+            const int qg = y % nqg, bkv = y / nqg;
+            const int b = bkv / Hkv, kvh = bkv % Hkv;
+            const int bhq0 = b * Hq + kvh * (Hq / Hkv) + qg * G;
+            for (int g = 0; g < G; g++) res |= head_mode[bhq0 + g] != 0;
+        }
+        const uint64_t mb = __ballot(live && !res), mm = __ballot(live && res);
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        if (lane == 0) {
+            wb[wave] = __popcll(mb);
+            wm_[wave] = __popcll(mm);
+        }
+        __syncthreads();
+        int ob = nb, om = nm;
+        for (int w = 0; w < wave; w++) {
+            ob += wb[w];
+            om += wm_[w];
+        }
+        if (live && !res) bin_list[ob + __popcll(mb & below)] = y;
+        if (live && res) mix_list[om + __popcll(mm & below)] = y;
+        for (int w = 0; w < kListThreads / 64; w++) {
+            nb += wb[w];
+            nm += wm_[w];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        lists[0] = nb;
+        lists[1] = nm;
+    }
+}
+
 __global__ void select_kernel(const float* e, uint8_t* modes, int n, float thr) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) modes[i] = e[i] >= thr ? 0 : 1;  // src/adaptive_precision.cu:133-144
@@ -930,15 +978,23 @@ size_t plan_bytes(int batch, int hq, const SplitPlan& p, int D) {
     return (size_t)batch * hq * p.n_splits * (D + 2) * sizeof(float);
 }
 
+// Per-head modes: after a plan's partials (at the next 256-byte boundary)
+// the workspace holds the two group lists of the mode launches: a 256-byte
+// header with the binary and mixed counts, then the binary groups' indices,
+// then the mixed groups' (int32, `groups` each).
+size_t list_offset(size_t partial_bytes) { return (partial_bytes + 255) & ~(size_t)255; }
+size_t list_bytes(int64_t groups) { return kListHeader + 2 * (size_t)groups * sizeof(int32_t); }
+
 // workspace of the split partials: the largest plan of any policy
-// plan_per_cu can return (per_cu = 0 .. kMaxPerCu)
+// plan_per_cu can return (per_cu = 0 .. kMaxPerCu), and the group lists
 size_t ws_bytes(int batch, int hq, int hkv, int S, int D, int cu = 0) {
     size_t n = plan_bytes(batch, hq, plan_splits(batch, hq, hkv, S, 0, cu), D);
     for (int per_cu = 1; per_cu <= kMaxPerCu; per_cu++) {
         const size_t b = plan_bytes(batch, hq, plan_splits(batch, hq, hkv, S, per_cu, cu), D);
         n = b > n ? b : n;
     }
-    return n;
+    const int G = pick_g(hq / hkv);
+    return list_offset(n) + list_bytes((int64_t)batch * hkv * ((hq / hkv) / G));
 }
 
 int validate_heads(int batch, int n_heads, int n_kv_heads, int seq_len, int kv_stride, int d) {
@@ -1018,11 +1074,15 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     BC_REQUIRE(workspace != nullptr && workspace_bytes >= need_ws, BC_ERR_WORKSPACE,
                "workspace of %zu bytes required, got %zu", need_ws, workspace_bytes);
     const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu);
-    // (the bound the launch needs: the partials of the plan it runs)
+    const int64_t groups = (int64_t)batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G);
+    // (the bound the launch needs: the partials of the plan it runs, and for
+    // per-head modes the group lists after them)
     const size_t plan_ws = plan_bytes(batch, n_heads, p, head_dim);
-    BC_REQUIRE(workspace_bytes >= plan_ws, BC_ERR_WORKSPACE,
-               "the split plan writes %zu bytes of partials, workspace holds %zu", plan_ws,
-               workspace_bytes);
+    const size_t plan_need =
+        mode == MODE_MIXED ? list_offset(plan_ws) + list_bytes(groups) : plan_ws;
+    BC_REQUIRE(workspace_bytes >= plan_need, BC_ERR_WORKSPACE,
+               "the split plan writes %zu bytes of partials and lists, workspace holds %zu",
+               plan_need, workspace_bytes);
     const int64_t cap = (int64_t)batch * n_kv_heads * kv_stride;
     AttnArgs a{};
     a.q = (const uint16_t*)q;
@@ -1054,27 +1114,45 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     // one split per group the matrix-core kernel normalises and writes the
     // output itself (no merge launch).
     if (direct_out != nullptr && p.n_splits == 1) a.out = (uint16_t*)direct_out;
-    // per-head modes on the matrix cores: the groups of binary heads only go
-    // to the binary kernel, which reads none of their residual bytes; both
-    // launches cover the grid and each skips the other's groups
-    if (!valu_forced() && mode == MODE_MIXED && bc::mfma_split_ok(head_dim, a.chunk)) {
-        if (!bc::launch_mfma_split(MODE_BINARY, head_dim, p.G, a, grid, st))
-            return bc::set_error(BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
-        const int rc = bc::check_launch("attention split (mfma, binary heads)");
+    // Per-head modes: the groups whose heads are all binary go to the binary
+    // kernel, which reads none of their residual bytes, the others to the
+    // mixed kernel.  A compaction launch lists each kind in order, and each
+    // mode launch's grid row y takes the y-th group of its list, so a
+    // launch's live workgroups come first in dispatch order and spread over
+    // the CUs evenly (rows past its count return at once).
+    int32_t* lists = nullptr;
+    if (mode == MODE_MIXED) {
+        lists = (int32_t*)((uint8_t*)workspace + list_offset(plan_ws));
+        hipLaunchKernelGGL(mode_groups_kernel, dim3(1), dim3(kListThreads), 0, st, head_mode,
+                           lists, (int)groups, (n_heads / n_kv_heads) / p.G, n_heads, n_kv_heads,
+                           p.G);
+        const int rc = bc::check_launch("per-head mode groups");
         if (rc != BC_OK) return rc;
+        a.group_list = lists + kListHeader / sizeof(int32_t);
+        a.group_count = lists;
     }
-    if (!valu_forced() && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st)) {
+    const bool mfma = !valu_forced() && bc::mfma_split_ok(head_dim, a.chunk) &&
+                      (head_dim == 64 || head_dim == 128 || head_dim == 256);
+    if (mode == MODE_MIXED) {
+        if (mfma) {
+            BC_REQUIRE(bc::launch_mfma_split(MODE_BINARY, head_dim, p.G, a, grid, st),
+                       BC_ERR_UNSUPPORTED, "head_dim %d", head_dim);
+        } else {
+            a.out = nullptr;
+            BC_DISPATCH_D(head_dim, launch_split_g, MODE_BINARY, p.G, a, grid, st);
+        }
+        const int rc = bc::check_launch("attention split (binary heads)");
+        if (rc != BC_OK) return rc;
+        a.group_list = lists + kListHeader / sizeof(int32_t) + groups;
+        a.group_count = lists + 1;
+    }
+    if (mfma && bc::launch_mfma_split(mode, head_dim, p.G, a, grid, st)) {
         if (wrote_out) *wrote_out = a.out != nullptr;
         return bc::check_launch("attention split (mfma)");
     }
     a.out = nullptr;
     // (the VALU kernel does not append; the append entry point checks first)
     BC_REQUIRE(app == nullptr, BC_ERR_UNSUPPORTED, "in-place append needs the MFMA kernel");
-    if (mode == MODE_MIXED) {
-        BC_DISPATCH_D(head_dim, launch_split_g, MODE_BINARY, p.G, a, grid, st);
-        const int rc = bc::check_launch("attention split (binary heads)");
-        if (rc != BC_OK) return rc;
-    }
     BC_DISPATCH_D(head_dim, launch_split_g, mode, p.G, a, grid, st);
     return bc::check_launch("attention split");
 }

@@ -471,23 +471,19 @@ void attn_mfma_kernel(AttnArgs a) {
 
     const int split = blockIdx.x;
     const int nqg = (a.Hq / a.Hkv) / G;
-    const int qg = blockIdx.y % nqg;
-    const int bkv = blockIdx.y / nqg;
+    // per-head modes: this launch's query-head groups come from its list
+    int grow = blockIdx.y;
+    if constexpr (MODE == MODE_BINARY || MODE == MODE_MIXED) {
+        if (a.group_list != nullptr) {
+            if (grow >= *a.group_count) return;
+            grow = a.group_list[grow];
+        }
+    }
+    const int qg = grow % nqg;
+    const int bkv = grow / nqg;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
     const int hq0 = kvh * (a.Hq / a.Hkv) + qg * G;
     const int bhq0 = b * a.Hq + hq0;
-    // Per-head modes run as two launches over the same grid and split plan:
-    // the binary kernel takes the groups of binary heads only (it reads no
-    // residual byte) and the mixed kernel the groups holding a compensated
-    // head; each workgroup of the other kind returns here, before any load.
-    if constexpr (MODE == MODE_BINARY || MODE == MODE_MIXED) {
-        if (a.head_mode != nullptr) {
-            bool any_res = false;
-#pragma unroll
-            for (int g = 0; g < G; g++) any_res |= a.head_mode[bhq0 + g] != 0;
-            if (MODE == MODE_BINARY ? any_res : !any_res) return;
-        }
-    }
 
     // the wave index is uniform: readfirstlane lets the compiler keep the tile
     // loop in scalar registers (a uniform loop, not an exec-masked one)

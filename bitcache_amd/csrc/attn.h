@@ -37,6 +37,12 @@ struct AttnArgs {
     int app_slot;
     // MODE_MIXED: [B*Hq] 0 = binary attention for that head, else compensated
     const uint8_t* head_mode;
+    // per-head modes run as two launches (binary kernel, mixed kernel), each
+    // over the query-head groups of its kind: grid row y takes group
+    // group_list[y] while y < *group_count, and returns otherwise (lists in
+    // the workspace, written by a compaction launch; null: row y is group y)
+    const int32_t* group_list;
+    const int32_t* group_count;
     // one split per group (n_splits == 1): when set, the kernel writes the
     // normalised output [B, Hq, D] fp16 here instead of its partial, and no
     // merge launch follows

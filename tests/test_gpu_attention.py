@@ -473,6 +473,9 @@ def test_gqa_equals_mha_on_repeated_kv(F, group, d):
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,d", [(2, 8, 8, 1500, 128), (2, 16, 4, 2000, 128),
                                           (1, 8, 2, 900, 64), (1, 4, 4, 700, 256),
+                                          # more query-head groups than one block of the
+                                          # group compaction takes at a time (1024)
+                                          (40, 32, 32, 130, 64), (48, 32, 8, 200, 128),
                                           # the VALU kernel's per-head modes
                                           (1, 4, 4, 500, 32), (1, 8, 2, 600, 96),
                                           (1, 4, 2, 300, 160), (1, 8, 4, 250, 224)])
