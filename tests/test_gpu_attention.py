@@ -201,6 +201,41 @@ def test_kv_stride_and_zero_length(F, H, Hkv, d):
     assert torch.count_nonzero(z) == 0
 
 
+@pytest.mark.parametrize("S", [(1 << 20) - 37, 1 << 21])
+def test_long_context_heads(F, S):
+    """One- and two-million-key heads (the split plan at its 2048-split cap, the
+    merge kernel's largest weight table, 32-bit buffer offsets per split, a
+    ragged last tile): compensated and binary attention against the torch-CPU
+    restatements at the fp bar."""
+    say(f"case long context S={S}")
+    B, H, d = 1, 2, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(S % 9973)
+    q = (torch.randn((B, H, d), generator=g, device="cuda") * 0.2).half()
+    k = (torch.randn((B * H * S, d), generator=g, device="cuda") * 0.2).half()
+    kb, kr = F.encode_fused(k)
+    del k
+    v = (torch.randn((B * H * S, d), generator=g, device="cuda") * 0.2).half()
+    vb, vr = F.encode_fused(v)
+    del v
+    comp = to_np(F.compensated_attention(q, kb, kr, vb, vr, B, H, S, d)).astype(np.float32)
+    binr = to_np(F.binary_attention(q, kb, vb, B, H, S, d)).astype(np.float32)
+    torch.set_num_threads(min(16, len(__import__("os").sched_getaffinity(0))))
+    n = B * H * S
+    kbc, krc, vbc, vrc, qc = kb.cpu(), kr.cpu(), vb.cpu(), vr.cpu(), q.cpu()
+    del kb, kr, vb, vr
+    rc = np.empty((B, H, d), np.float32)
+    rb = np.empty((B, H, d), np.float32)
+    for h in range(H):
+        args = blob_head_tensors(kbc, krc, vbc, vrc, n, d, h * S, S)
+        rc[0, h] = O.compensated_attention_torch_cpu(qc[0, h], *args).float().numpy()
+        rb[0, h] = O.binary_attention_torch_cpu(qc[0, h][None], args[0], args[1], args[4],
+                                                args[5])[0].float().numpy()
+    close(comp, rc, what=f"compensated S={S}")
+    close(binr, rb, what=f"binary S={S}")
+    torch.cuda.empty_cache()
+
+
 # (B, Hq, Hkv, S): MHA, GQA, and a group of 32 heads (two head batches per workgroup row)
 @pytest.mark.parametrize("shape", [(2, 8, 8, 1500), (2, 8, 2, 1500), (1, 32, 1, 700)])
 def test_binary_scores_exact(F, shape):
