@@ -192,7 +192,8 @@ def bench_c2(args, torch, _C, W):
         "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(alg / wall / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": traffic_from_profiles("traffic_c2_c5_counters.md", "traffic_bytes_per_step_c2"),
-                     "kernel": "attention step (split + combine), wall clock"},
+                     "kernel": "attention step, wall clock (one 8-wave workgroup per head writes the "
+                               "output: one launch, no merge)"},
         "kendall_tau": {"vs": "exact q.k (fp32) per (b, h), all 32768 keys",
                         "tau_a_mean": round(sum(ta) / len(ta), 4), "tau_a_min": round(min(ta), 4),
                         "tau_b_mean": round(sum(tb) / len(tb), 4), "tau_b_min": round(min(tb), 4),

@@ -963,6 +963,28 @@ int plan_per_cu(int mode, int D, int G) {
 // reference kernel
 constexpr int kPlanFixed = 0;
 
+// Binary MHA attention at d = 128 whose heads fill the CUs in whole rounds:
+// one workgroup of kWideWaves waves per head takes all its keys (wave w the
+// tiles w, w + 8, ...), merges its waves and writes the output, so the call
+// writes no partials and launches no merge.  Measured on the 256-head, 32K-key
+// binary step: 56.0 -> 47.1-48.1 us (the 4-wave plan: two workgroups per CU
+// and the merge launch); 16-wave workgroups 50.4-51.0 us.  Contexts up to
+// kWideMaxKeys (each wave's sums cover at most 16K keys, as in the split
+// plans).  The compensated kernel gains nothing this way (one round of
+// 12-wave workgroups at 64K keys: kernel 425 against 406 us, step 430 against
+// 428 us), so it keeps its split plans.  BITCACHE_WIDE=0 turns this off
+// (tuning).
+constexpr int kWideWaves = 8;
+constexpr int kWideMaxKeys = 131072;
+bool wide_plan(int mode, int D, int G, int64_t groups, int S, int cu) {
+    static const bool off = [] {
+        const char* e = getenv("BITCACHE_WIDE");
+        return e != nullptr && atoi(e) == 0;
+    }();
+    return !off && mode == MODE_BINARY && G == 1 && D == 128 && S > 0 && S <= kWideMaxKeys &&
+           cu > 0 && groups >= cu && groups % cu == 0;
+}
+
 // BITCACHE_VALU_ATTENTION=1 selects the VALU split kernel for every head dim
 bool valu_forced() {
     static const bool forced = [] {
@@ -1133,6 +1155,19 @@ int run_partial(int mode, const void* q, const void* k_bin, const void* k_res, c
     }
     const bool mfma = !valu_forced() && bc::mfma_split_ok(head_dim, a.chunk) &&
                       (head_dim == 64 || head_dim == 128 || head_dim == 256);
+    // one wide workgroup per head (wide_plan): no partials, no merge launch
+    if (mfma && direct_out != nullptr && app == nullptr &&
+        wide_plan(mode, head_dim, p.G, groups, seq_len, bc::device_cu_count())) {
+        AttnArgs w = a;
+        w.n_splits = 1;
+        w.chunk = (seq_len + 63) / 64 * 64;
+        w.out = (uint16_t*)direct_out;
+        if (bc::mfma_split_ok(head_dim, w.chunk) &&
+            bc::launch_mfma_split(mode, head_dim, 1, w, dim3(1, (unsigned)groups), st, kWideWaves)) {
+            if (wrote_out) *wrote_out = true;
+            return bc::check_launch("attention (wide workgroups)");
+        }
+    }
     if (mode == MODE_MIXED) {
         if (mfma) {
             BC_REQUIRE(bc::launch_mfma_split(MODE_BINARY, head_dim, p.G, a, grid, st),
@@ -1213,7 +1248,13 @@ extern "C" int bc_attention_split_plan(int mode, int batch, int n_heads, int n_k
     BC_REQUIRE(n_splits && partial_bytes && workspace_bytes, BC_ERR_INVALID_ARGUMENT,
                "null output");
     const int per_cu = plan_per_cu(mode, head_dim, pick_g(n_heads / n_kv_heads));
-    const SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu, cu_count);
+    SplitPlan p = plan_splits(batch, n_heads, n_kv_heads, seq_len, per_cu, cu_count);
+    const int64_t groups = (int64_t)batch * n_kv_heads * ((n_heads / n_kv_heads) / p.G);
+    if (wide_plan(mode, head_dim, p.G, groups, seq_len, cu_count > 0 ? cu_count : bc::device_cu_count())) {
+        // (one wide workgroup per head; no partials are written)
+        p.n_splits = 1;
+        p.chunk = (seq_len + 63) / 64 * 64;
+    }
     *n_splits = p.n_splits;
     *partial_bytes = plan_bytes(batch, n_heads, p, head_dim);
     *workspace_bytes = ws_bytes(batch, n_heads, n_kv_heads, seq_len, head_dim, cu_count);

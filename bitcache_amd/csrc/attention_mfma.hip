@@ -195,13 +195,13 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Query preparation of one workgroup (256 threads), spread over all threads:
+// Query preparation of one workgroup (NT threads), spread over all threads:
 // the query as floats and its sign words (a wave ballot per 64 elements);
 // scale_q (sequential fp32 order, element 0 first) and the fixed-point step
 // per head; q_int = rint(q / step) per element (in place of the floats); then
 // the balanced int4 digit words (one (word, digit) pair per thread) and the
 // int8 MFMA operand words (the fixed-point parts only for residual modes).
-template <int D, int G, bool KMF, bool RES, int NQ>
+template <int D, int G, bool KMF, bool RES, int NT, int NQ>
 __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float* qf) {
     static_assert((G * D) % 64 == 0, "whole waves of query elements");
     const int tid = threadIdx.x, lane = tid & 63;
@@ -210,10 +210,10 @@ __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float
     // the three int8 planes of q_int per element (int8 MFMA operands)
     __shared__ __attribute__((aligned(8))) uint8_t pbytes[KMF ? 3 : 1][KMF ? G * D : 8];
     // floats, sign words (wave ballots) and each wave's max |q| (its 64
-    // elements lie in one head); element tid + 256j was loaded into qpre[j]
+    // elements lie in one head); element tid + NT j was loaded into qpre[j]
 #pragma unroll
     for (int j = 0; j < NQ; j++) {
-        const int i = tid + 256 * j;
+        const int i = tid + NT * j;
         if (i >= G * D) break;   // (whole waves)
         const float x = h2f(qpre[j]);
         qf[i] = x;
@@ -258,7 +258,7 @@ __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float
     // q_int over the floats (each thread converts the elements it reads) and
     // its balanced int8 planes, q_int = p0 + 256 p1 + 65536 p2, p_i in [-128, 127]
     int* qint = (int*)qf;
-    for (int i = tid; i < G * D; i += 256) {
+    for (int i = tid; i < G * D; i += NT) {
         const int t = (int)__builtin_rintf(qf[i] / (qd.dq[i / D] * (1.0f / 256.0f)));
         qint[i] = t;
         if constexpr (KMF) {
@@ -275,7 +275,7 @@ __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float
     // base 16: t = sum_j d_j 16^j, d_j in [-8, 7]).  Four threads per word
     // (a DPP quad), two elements each; the quad ORs its nibbles together.
     static_assert((G * D / 2) % 4 == 0, "whole quads per digit word");
-    for (int e = tid; e < G * (D / 2); e += 256) {
+    for (int e = tid; e < G * (D / 2); e += NT) {
         const int gw = e >> 2, q = e & 3, g = gw / (D / 8), w = gw % (D / 8);
         uint32_t word[6];
 #pragma unroll
@@ -309,7 +309,7 @@ __device__ void prep_digits(const uint16_t (&qpre)[NQ], QDigits<D, G>& qd, float
         // bytes of the 8 plane bytes at dim 32 (q + 4 pc) + 8 (2h + rr)
         constexpr int NPC = D / 128;
         constexpr bool LO_COLS = 3 * G <= 16;
-        for (int e = tid; e < NPC * 2 * 64; e += 256) {
+        for (int e = tid; e < NPC * 2 * 64; e += NT) {
             const int pc = e / 128, h = (e / 64) & 1, ln = e & 63;
             const int col = ln & 15, qg4 = ln >> 4;
             int gv = 0, pv = -1;   // the lane's column: plane pv of head gv (pv < 0: zeros)
@@ -405,8 +405,11 @@ __device__ __forceinline__ int row_group_sum(int v) {
     return v;
 }
 
-template <int D, int G, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Occupancy<D, G, MODE>::kWaves)))
+// NW waves per workgroup (4, or 8 to 16 for a wide workgroup that takes all
+// keys of its group: one split, no merge launch); wave w takes tiles w, w + NW,
+// w + 2 NW, ... of the key range, and the epilogue merges the NW waves.
+template <int D, int G, int MODE, int NW = 4>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(Occupancy<D, G, MODE>::kWaves)))
 void attn_mfma_kernel(AttnArgs a) {
     constexpr int NB = D / 16;   // nibble dim-blocks (16 dims each)
     constexpr int NH = D / 64;   // sign blocks (64 dims each)
@@ -457,17 +460,17 @@ void attn_mfma_kernel(AttnArgs a) {
 
     __shared__ QDigits<D, G> qd;
     __shared__ __attribute__((aligned(16))) float qf[G * D];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_st0[4][WL::kStage];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_st1[4][PIPE ? WL::kStage : 16];
-    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[4][(I8 && !RES) ? 8 : WL::kWeightBytes / 2];
-    __shared__ __attribute__((aligned(16))) int8_t lds_w8[4][I8 ? 4 * G * kW8Stride : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_st0[NW][WL::kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_st1[NW][PIPE ? WL::kStage : 16];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_wts[NW][(I8 && !RES) ? 8 : WL::kWeightBytes / 2];
+    __shared__ __attribute__((aligned(16))) int8_t lds_w8[NW][I8 ? 4 * G * kW8Stride : 16];
     // (int8 path) per wave and head, the float sums of the keys before the
     // last rescale, [head][D] in the epilogue's dim order
-    __shared__ __attribute__((aligned(16))) float lds_bank[4][I8 ? G * D : 4];
-    __shared__ __attribute__((aligned(16))) int lds_rd[4][WL::kRdInts];
-    __shared__ __attribute__((aligned(16))) int lds_rdlo[4][(KMF && 3 * G <= 16) ? WL::kRdInts : 1];
-    __shared__ float wofs[4][G];
-    __shared__ float wm[4][G], wlsum[4][G], wsc[4];
+    __shared__ __attribute__((aligned(16))) float lds_bank[NW][I8 ? G * D : 4];
+    __shared__ __attribute__((aligned(16))) int lds_rd[NW][WL::kRdInts];
+    __shared__ __attribute__((aligned(16))) int lds_rdlo[NW][(KMF && 3 * G <= 16) ? WL::kRdInts : 1];
+    __shared__ float wofs[NW][G];
+    __shared__ float wm[NW][G], wlsum[NW][G], wsc[NW];
 
     const int split = blockIdx.x;
     const int nqg = (a.Hq / a.Hkv) / G;
@@ -618,13 +621,14 @@ void attn_mfma_kernel(AttnArgs a) {
     // the workgroup that appends a token), and the query preparation runs
     // while that tile is in flight: it waits only for the older query loads,
     // and its barriers wait for LDS traffic only.
-    constexpr int NQ = (G * D + 255) / 256;
+    constexpr int NT = NW * 64;
+    constexpr int NQ = (G * D + NT - 1) / NT;
     uint16_t qpre[NQ];
     {
         const uint16_t* qb = a.q + (int64_t)bhq0 * D;
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
-            const int i = (int)threadIdx.x + 256 * j;
+            const int i = (int)threadIdx.x + NT * j;
             qpre[j] = i < G * D ? qb[i] : (uint16_t)0;
         }
     }
@@ -643,7 +647,7 @@ void attn_mfma_kernel(AttnArgs a) {
         issue_v(0, t_first);
     }
     __builtin_amdgcn_sched_barrier(0);
-    prep_digits<D, G, KMF, RES>(qpre, qd, qf);
+    prep_digits<D, G, KMF, RES, NT>(qpre, qd, qf);
 
     // In-place append: the workgroup whose key range holds the new token's slot
     // encodes the token's K and V vectors into the cache first (wave 0, lane
@@ -1443,14 +1447,14 @@ void attn_mfma_kernel(AttnArgs a) {
         if (t < key_end) {
             KRegs<D> ra, rb, rc, rd;
             load_k(ra, t);
-            load_k(rb, t + 4 * 64);
+            load_k(rb, t + NW * 64);
             gather(ra, t, 0);
             __builtin_amdgcn_s_waitcnt(0);
             for (;;) {
-                const int t1 = t + 4 * 64;
+                const int t1 = t + NW * 64;
                 gather(rb, t1, 1);
-                load_k(rc, t + 8 * 64);
-                load_k(rd, t + 12 * 64);
+                load_k(rc, t + 2 * NW * 64);
+                load_k(rd, t + 3 * NW * 64);
                 process(ra, t, 0);
                 if (t1 >= key_end) break;
                 // ra is free: it takes the popcounts and scales of tile t + 512
@@ -1458,9 +1462,9 @@ void attn_mfma_kernel(AttnArgs a) {
                 ra.pcw[0] = rc.pcw[0]; ra.pcw[1] = rc.pcw[1]; ra.pcw[2] = rc.pcw[2]; ra.pcw[3] = rc.pcw[3];
                 ra.sk = rc.sk;
                 ra.svv = rc.svv;
-                gather(ra, t + 8 * 64, 0);
+                gather(ra, t + 2 * NW * 64, 0);
                 process(rb, t1, 1);
-                t += 8 * 64;
+                t += 2 * NW * 64;
                 if (t >= key_end) break;
                 __builtin_amdgcn_s_waitcnt(0);
                 rb.pcw[0] = rd.pcw[0]; rb.pcw[1] = rd.pcw[1]; rb.pcw[2] = rd.pcw[2]; rb.pcw[3] = rd.pcw[3];
@@ -1472,7 +1476,7 @@ void attn_mfma_kernel(AttnArgs a) {
         }
     } else if (!PIPE) {
         bool issued = early;   // (the first tile's loads went out before the preparation)
-        for (; t < key_end; t += 4 * 64) {
+        for (; t < key_end; t += NW * 64) {
             if (!issued) {
                 load_k(ka, t);
                 issue_v(0, t);
@@ -1489,17 +1493,17 @@ void attn_mfma_kernel(AttnArgs a) {
         }
         __builtin_amdgcn_s_waitcnt(0);
         for (;;) {
-            int tp = t + 4 * 64;
+            int tp = t + NW * 64;
             load_k(kb, tp);
             issue_v(1, tp);
             process(ka, t, 0);
-            t += 4 * 64;
+            t += NW * 64;
             if (t >= key_end) break;
-            tp = t + 4 * 64;
+            tp = t + NW * 64;
             load_k(ka, tp);
             issue_v(0, tp);
             process(kb, t, 1);
-            t += 4 * 64;
+            t += NW * 64;
             if (t >= key_end) break;
             __builtin_amdgcn_s_waitcnt(0);
         }
@@ -1527,14 +1531,14 @@ void attn_mfma_kernel(AttnArgs a) {
     // per head: the maximum M over the waves, each wave's factor
     // 2^(m_w - M) * 2^-wexp_w (0 for a wave without keys) and the total l
     // (published by the first barrier of the head batches below)
-    __shared__ float mfac[4][G], hsum[2][G];
+    __shared__ float mfac[NW][G], hsum[2][G];
     __syncthreads();
     if (threadIdx.x < G) {
         const int g = threadIdx.x;
         float M = -INFINITY;
-        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][g]);
         float lv = 0.0f;
-        for (int w = 0; w < 4; w++) {
+        for (int w = 0; w < NW; w++) {
             const bool live = M != -INFINITY && wm[w][g] != -INFINITY;
             const float f = live ? exp2f(wm[w][g] - M) : 0.0f;
             mfac[w][g] = f * wsc[w];
@@ -1630,7 +1634,7 @@ void attn_mfma_kernel(AttnArgs a) {
             const int hs2 = i / D, e = i % D, g = g0 + hs2;
             float accv = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NW; w++) {
                 const float* aw = (const float*)lds_st0[w];
                 float v = aw[(0 * HP + hs2) * D + e];
                 if (RES) v += aw[(1 * HP + hs2) * D + e];
@@ -1654,6 +1658,19 @@ void attn_mfma_kernel(AttnArgs a) {
     }
 }
 
+// Wide workgroups (one split per group, the output written directly): MHA
+// binary attention at d = 128 with 8 waves; false for any other request.
+template <int D, int G>
+bool launch_wide(int mode, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
+    if constexpr (G == 1 && D == 128) {
+        if (mode == MODE_BINARY && nw == 8) {
+            hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a);
+            return true;
+        }
+    }
+    return false;
+}
+
 template <int D, int G>
 void launch_dg(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
     if (mode == MODE_BINARY)
@@ -1664,6 +1681,11 @@ void launch_dg(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_MIXED>), grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_ADAPTIVE>), grid, dim3(256), 0, st, a);
+}
+
+template <int D>
+bool launch_wide_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
+    return G == 1 && launch_wide<D, 1>(mode, a, grid, st, nw);
 }
 
 template <int D>
@@ -1728,16 +1750,17 @@ int mfma_wgs_per_cu(int mode, int D, int G) {
 bool mfma_split_ok(int D, int64_t chunk) {
     if (D != 64 && D != 128 && D != 256) return false;
     // buffer offsets are 32-bit and relative to a split's key range; the
-    // prefetches reach up to 12 tiles (768 keys) past its end.  The int8
+    // prefetches reach up to 17 tiles (1088 keys) past its end.  The int8
     // value path adds at most 2^16 per tile to an int32 accumulator: a wave
     // takes at most 2^15 tiles (a split below 2^23 keys)
-    return (chunk + 1024) * (D / 2) + 4096 < ((int64_t)1 << 31) && chunk < ((int64_t)1 << 23);
+    return (chunk + 2048) * (D / 2) + 4096 < ((int64_t)1 << 31) && chunk < ((int64_t)1 << 23);
 }
 
-bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st) {
+bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
     if (!mfma_split_ok(D, a.chunk)) return false;
     // adaptive mode reads the popcounts stored by the selection passes
     if (mode == MODE_ADAPTIVE && a.pcs == nullptr) return false;
+    if (nw != 4) return D == 128 && launch_wide_d<128>(mode, G, a, grid, st, nw);
     switch (D) {
         case 64: launch_d<64>(mode, G, a, grid, st); return true;
         case 128: launch_d<128>(mode, G, a, grid, st); return true;

@@ -65,7 +65,7 @@ struct __attribute__((aligned(G * sizeof(P)))) PcPack {
 
 // MFMA value-phase kernels (attention_mfma.hip): true if (D, G, mode) is
 // handled there and the launch was issued.
-bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st);
+bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw = 4);
 // True if the MFMA kernels handle head_dim D with splits of `chunk` keys.
 bool mfma_split_ok(int D, int64_t chunk);
 // Resident workgroups per CU of the MFMA kernel of (mode, D, G) on the current

@@ -151,6 +151,8 @@ int bc_attention_workspace_size(int batch, int n_heads, int n_kv_heads, int seq_
 /* The key-split plan an attention call of this shape launches: n_splits per
  * (b, query-head group), the bytes of split partials it writes and the
  * workspace bc_attention_workspace_size reports (always >= partial_bytes).
+ * (A plan of one split writes the output from its attention kernel; then
+ * partial_bytes is what that split's partials would take.)
  * mode: BC_MODE_*; cu_count 0 plans for the current device, > 0 for a device
  * of that many CUs.  Allocates nothing and launches nothing.  No counterpart
  * in the reference; a diagnostic for callers sizing workspaces and for tests. */

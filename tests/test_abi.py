@@ -213,6 +213,36 @@ def test_workspace_covers_every_split_plan(lib):
              ctypes.byref(total)) == BC_ERR_INVALID_ARGUMENT
 
 
+def test_wide_binary_plan(lib):
+    """Binary MHA attention at d = 128 whose heads fill the CUs in whole rounds
+    (and whose context is at most 131072 keys) plans one split per head: one
+    wide workgroup takes all of a head's keys and writes the output.  Other
+    modes, GQA groups, other head dims, longer contexts and head counts that
+    leave a round partly filled keep the split plans."""
+    size_t = ctypes.c_size_t
+    f = lib.bc_attention_split_plan
+    f.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(size_t),
+                                       ctypes.POINTER(size_t)]
+    n, part, total = ctypes.c_int(0), size_t(0), size_t(0)
+
+    def splits(mode, B, Hq, Hkv, S, d, cu):
+        assert f(mode, B, Hq, Hkv, S, d, cu, ctypes.byref(n), ctypes.byref(part),
+                 ctypes.byref(total)) == BC_OK, lib.bc_last_error()
+        assert part.value == B * Hq * n.value * (d + 2) * 4 <= total.value
+        return n.value
+
+    assert splits(0, 8, 32, 32, 32768, 128, 256) == 1        # c2: 256 heads on 256 CUs
+    assert splits(0, 16, 32, 32, 32768, 128, 256) == 1       # two rounds
+    assert splits(0, 4, 32, 32, 131072, 128, 128) == 1       # the longest wide context
+    assert splits(0, 8, 32, 32, 32768, 128, 80) > 1          # 256 heads on 80 CUs
+    assert splits(0, 8, 32, 32, 32768, 128, 512) > 1         # half a round
+    assert splits(0, 4, 32, 32, 131136, 128, 128) > 1        # past the wide context
+    assert splits(0, 8, 32, 32, 32768, 64, 256) > 1          # another head dim
+    assert splits(0, 8, 32, 8, 32768, 128, 64) > 1           # GQA groups
+    assert splits(1, 8, 32, 32, 32768, 128, 256) > 1         # compensated
+    assert splits(3, 8, 32, 32, 32768, 128, 256) > 1         # per-head modes
+
+
 def test_extension_rejects_cpu_tensors():
     torch = pytest.importorskip("torch")
     import bitcache_amd

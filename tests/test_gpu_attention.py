@@ -117,9 +117,12 @@ def test_many_groups_and_split_phase_api(F, shape):
     close(to_np(outpb).astype(np.float32), refb, what=f"split-phase binary {shape}")
     if shape == LAUNCH_SHAPES[0]:
         # 1536 MHA groups fill a round with one split each, in both plans: the
-        # full call writes the output from the split kernel (no merge launch),
-        # bit for bit what the merge of the single partial gives
-        assert torch.equal(out, outp) and torch.equal(outb, outpb)
+        # full compensated call writes the output from the split kernel (no
+        # merge launch), bit for bit what the merge of the single partial
+        # gives.  (The full binary call runs one 8-wave workgroup per head when
+        # the heads fill the CUs in whole rounds, which sums in another order:
+        # checked against the oracle above.)
+        assert torch.equal(out, outp)
 
 
 def make_rising(B, Hq, Hkv, S, d, seed):
