@@ -401,23 +401,63 @@ __global__ __launch_bounds__(256) void collect_kernel(SelArgs a) {
                 st.sc[u] = *(const bc_v4u*)(scales + 8 * oc);
             }
         };
+        // the fast path's bounds: a head without a bucket (live false) gets
+        // an empty range
+        float flo_f[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) flo_f[g] = live[g] ? flo[g] : INFINITY;
+        auto pc_of = [&](const Stage& st, int u, int j, int g) {
+            constexpr int pb = (int)sizeof(P);
+            const int byte = (j * G + g) * pb;
+            return (st.pw[u][byte / 4] >> (8 * (byte % 4))) & ((1u << (8 * pb)) - 1u);
+        };
         auto run = [&](const Stage& st, int o) {
 #pragma unroll
             for (int u = 0; u < UP; u++) {
                 const int oo = o + u * 256;
+                float sk[8];
+                bool nonfinite = false;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const int s = 8 * oo + j;
                     const uint32_t sw = st.sc[u][j >> 1];
-                    const float sk = h2f((uint16_t)((j & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
-                    int pc[G];
+                    sk[j] = h2f((uint16_t)((j & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+                    const bool valid = oo < o1 && 8 * oo + j < k1;
+                    nonfinite |= valid && !finite_scale(sk[j]);
+                }
+                if (__ballot(nonfinite) == 0ull) {
+                    // every scale of the wave's octets is finite: exact float
+                    // scores against the bucket's float range; a key past the
+                    // chunk gets a NaN scale, so its compares fail
 #pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        constexpr int pb = (int)sizeof(P);
-                        const int byte = (j * G + g) * pb;
-                        pc[g] = (int)((st.pw[u][byte / 4] >> (8 * (byte % 4))) & ((1u << (8 * pb)) - 1u));
+                    for (int j = 0; j < 8; j++) {
+                        const int s = 8 * oo + j;
+                        const float skj = (oo < o1 && s < k1) ? sk[j] : __builtin_nanf("");
+                        const float sk2 = 2.0f * skj, nd = -(float)D * skj;
+#pragma unroll
+                        for (int g = 0; g < G; g++) {
+                            const float sc = fmaf((float)pc_of(st, u, j, g), sk2, nd);
+                            const bool in = sc > flo_f[g] && sc <= fhi[g];
+                            const uint64_t m = __ballot(in);
+                            if (m != 0ull) {
+                                if (in) {
+                                    const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                                    stg[wave][g][rc[g] + below] =
+                                        (((ordered_bits(sc) >> 6) & ((1u << kLowBits) - 1u)) << 16) | (uint32_t)(s - k0);
+                                }
+                                rc[g] += (uint32_t)__builtin_popcountll(m);
+                            }
+                        }
                     }
-                    take(pc, sk, s, oo < o1 && s < k1);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int s = 8 * oo + j;
+                        int pc[G];
+#pragma unroll
+                        for (int g = 0; g < G; g++) pc[g] = (int)pc_of(st, u, j, g);
+                        take(pc, sk[j], s, oo < o1 && s < k1);
+                    }
                 }
                 flush();
             }
