@@ -6,7 +6,9 @@
 //   1. hist_kernel: the popcounts of every key from the K sign planes, stored
 //      (one byte per query head and key, two for d = 256: the later launches
 //      and the attention pass read them instead of the d/8-byte sign rows),
-//      and per key chunk a histogram of the keys' top 13 bits (16-bit counts);
+//      and per key chunk a histogram of the keys' top 13 bits (16-bit counts;
+//      only its 64-word blocks holding a count are stored, with a mask of
+//      them: scores fill a few binades, so most blocks are empty);
 //   2. pick_kernel: per (b, head), sums the chunk histograms and picks the
 //      bucket (top-13-bit digit) holding the k-th largest key; `remain` keys
 //      are still to be taken from it;
@@ -31,7 +33,8 @@
 // prefix (see key_floor), which order like the keys; a wave holding a
 // non-finite scale compares the keys themselves.
 //
-// Workspace: chunk histograms [B*Hq][hsplit][8192] u16 | prefix [B*Hq] u32
+// Workspace: chunk histograms [B*Hq][hsplit][8192] u16 | their block masks
+//   [B*Hq][hsplit] u64 | prefix [B*Hq] u32
 //   | remain [B*Hq] i32 | cutoff [B*Hq] i32 | popcounts [B*Hq/G][pcs_stride(S)][G]
 //   | bucket lists [B*Hq][nsplit][4 waves][wcap] u32 | list counts [B*Hq][nsplit][4] u32
 //   | attention partials.
@@ -64,7 +67,9 @@ struct SelArgs {
     int nsplit, chunk;   // key chunks of the collect pass (chunk: a multiple of 64, <= kMaxChunk)
     int wcap;            // list entries per (head, chunk, wave)
     uint32_t* hist;      // [B*Hq][hsplit][kTopBins / 2] each key chunk's top-digit histogram
-                         // (bin b: half b & 1 of word b >> 1)
+                         // (bin b: half b & 1 of word b >> 1); only the 64-word blocks
+                         // whose bit is set in hmask are stored (the others are 0)
+    uint64_t* hmask;     // [B*Hq][hsplit] bit k: block k (words 64k .. 64k + 63) holds a count
     uint32_t* prefix;    // [B*Hq] bucket digit << kTopShift, then the threshold T
     int32_t* remain;     // [B*Hq] keys still to take from the bucket, then at T
     int32_t* cutoff;     // [B*Hq]
@@ -106,7 +111,7 @@ __device__ __forceinline__ uint32_t key_of_pc(int pc, float sk) {
 template <int D, int G>
 __global__ __launch_bounds__(kHistThreads) void hist_kernel(SelArgs a) {
     __shared__ uint32_t qs[G][D / 32];
-    __shared__ uint32_t h[G][kTopBins / 2];
+    __shared__ __attribute__((aligned(16))) uint32_t h[G][kTopBins / 2];
     const int nqg = (a.Hq / a.Hkv) / G;
     const int qg = blockIdx.y % nqg, bkv = blockIdx.y / nqg;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
@@ -179,9 +184,41 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(SelArgs a) {
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < G * kTopBins / 2; i += blockDim.x) {
-        const int g = i / (kTopBins / 2), w = i % (kTopBins / 2);
-        a.hist[((int64_t)(bhq0 + g) * a.hsplit + blockIdx.x) * (kTopBins / 2) + w] = h[g][w];
+    // Per head: thread t holds words 8t .. 8t + 7 (block t / 8); a block is
+    // stored, as whole lines, when one of its words holds a count, and the
+    // head's mask of such blocks goes with it (the pick reads only those)
+    static_assert(kTopBins / 2 == 8 * kHistThreads && kTopBins / 2 / 64 == 64, "one 64-bit block mask per head");
+    __shared__ uint32_t bm[G][kHistThreads / 64];   // per head and wave: its 8 blocks' bits
+    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const bc_v4u x0 = *(const bc_v4u*)&h[g][8 * threadIdx.x];
+        const bc_v4u x1 = *(const bc_v4u*)&h[g][8 * threadIdx.x + 4];
+        const bool nz = (x0[0] | x0[1] | x0[2] | x0[3] | x1[0] | x1[1] | x1[2] | x1[3]) != 0u;
+        const uint64_t lanes = __ballot(nz);   // lanes 8k .. 8k + 7: block 8 wv + k
+        if (ln == 0) {
+            uint32_t bits = 0u;
+#pragma unroll
+            for (int k = 0; k < 8; k++) bits |= ((lanes >> (8 * k)) & 0xFFull) != 0ull ? (1u << k) : 0u;
+            bm[g][wv] = bits;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int64_t row = (int64_t)(bhq0 + g) * a.hsplit + blockIdx.x;
+        const int blk = threadIdx.x >> 3;   // 0 .. 63
+        if ((bm[g][blk >> 3] >> (blk & 7)) & 1u) {
+            bc_v4u* dst = (bc_v4u*)(a.hist + row * (kTopBins / 2) + 8 * threadIdx.x);
+            dst[0] = *(const bc_v4u*)&h[g][8 * threadIdx.x];
+            dst[1] = *(const bc_v4u*)&h[g][8 * threadIdx.x + 4];
+        }
+        if (threadIdx.x == 0) {
+            uint64_t m = 0ull;
+#pragma unroll
+            for (int w = 0; w < kHistThreads / 64; w++) m |= (uint64_t)bm[g][w] << (8 * w);
+            a.hmask[row] = m;
+        }
     }
 }
 
@@ -195,11 +232,15 @@ __global__ __launch_bounds__(256) void pick_kernel(SelArgs a, int top_k) {
     __shared__ uint32_t part[256];
     const int bhq = blockIdx.x;
     const uint32_t* h = a.hist + (int64_t)bhq * a.hsplit * (kTopBins / 2);
+    const uint64_t* hm = a.hmask + (int64_t)bhq * a.hsplit;
     const int b0 = kTopBins - kPer * ((int)threadIdx.x + 1);
+    const int blk = (b0 / 2) / 64;   // this thread's 16 words lie in one 64-word block
+    static_assert(kPer == 32, "16 words per thread, within one block");
     uint32_t cnt[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; j++) cnt[j] = 0u;
     for (int c = 0; c < a.hsplit; c++) {
+        if (((hm[c] >> blk) & 1ull) == 0ull) continue;   // (a block never stored: all zero)
         const bc_v4u* src = (const bc_v4u*)(h + (int64_t)c * (kTopBins / 2) + b0 / 2);
 #pragma unroll
         for (int v = 0; v < kPer / 8; v++) {
@@ -802,7 +843,7 @@ Chunks chunks_for(int batch, int hq, int hkv, int S) {
 }
 
 struct Layout {
-    size_t hist, prefix, remain, cutoff, pcs, lists, counts, attn, total;
+    size_t hist, hmask, prefix, remain, cutoff, pcs, lists, counts, attn, total;
 };
 
 Layout layout(int batch, int hq, int hkv, int S, int d) {
@@ -812,7 +853,8 @@ Layout layout(int batch, int hq, int hkv, int S, int d) {
     const size_t regions = bh * (size_t)c.nsplit * 4;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.hist = 0;
-    L.prefix = al(L.hist + bh * (size_t)c.hsplit * (kTopBins / 2) * 4);
+    L.hmask = al(L.hist + bh * (size_t)c.hsplit * (kTopBins / 2) * 4);
+    L.prefix = al(L.hmask + bh * (size_t)c.hsplit * 8);
     L.remain = al(L.prefix + bh * 4);
     L.cutoff = al(L.remain + bh * 4);
     L.pcs = al(L.cutoff + bh * 4);
@@ -890,6 +932,7 @@ extern "C" int bc_adaptive_attention(const void* q, const void* k_bin, const voi
     a.S = seq_len;
     a.kv_stride = kv_stride;
     a.hist = (uint32_t*)(ws + L.hist);
+    a.hmask = (uint64_t*)(ws + L.hmask);
     a.prefix = (uint32_t*)(ws + L.prefix);
     a.remain = (int32_t*)(ws + L.remain);
     a.cutoff = (int32_t*)(ws + L.cutoff);
