@@ -963,13 +963,15 @@ int plan_per_cu(int mode, int D, int G) {
 // reference kernel
 constexpr int kPlanFixed = 0;
 
-// Binary MHA attention at d = 128 whose heads fill the CUs in whole rounds:
-// one workgroup of kWideWaves waves per head takes all its keys (wave w the
-// tiles w, w + 8, ...), merges its waves and writes the output, so the call
-// writes no partials and launches no merge.  Measured on the 256-head, 32K-key
-// binary step: 56.0 -> 47.1-48.1 us (the 4-wave plan: two workgroups per CU
-// and the merge launch); 16-wave workgroups 50.4-51.0 us.  Contexts up to
-// kWideMaxKeys (each wave's sums cover at most 16K keys, as in the split
+// Binary MHA attention at d = 128 with one head per CU: one workgroup of
+// kWideWaves waves per head takes all its keys (wave w the tiles w, w + 8,
+// ...), merges its waves and writes the output, so the call writes no
+// partials and launches no merge.  Measured on the 256-head, 32K-key binary
+// step: 52.8-56.0 -> 47.0-48.1 us (the 4-wave plan: two workgroups per CU and
+// the merge launch); 16-wave workgroups 50.4-51.0 us.  With two or more heads
+// per CU the split plans already launch no merge and the wide plan measured
+// within noise of them (-4% to +2%), so it is left to one round.  Contexts up
+// to kWideMaxKeys (each wave's sums cover at most 16K keys, as in the split
 // plans).  The compensated kernel gains nothing this way (one round of
 // 12-wave workgroups at 64K keys: kernel 425 against 406 us, step 430 against
 // 428 us), so it keeps its split plans.  BITCACHE_WIDE=0 turns this off
@@ -982,7 +984,7 @@ bool wide_plan(int mode, int D, int G, int64_t groups, int S, int cu) {
         return e != nullptr && atoi(e) == 0;
     }();
     return !off && mode == MODE_BINARY && G == 1 && D == 128 && S > 0 && S <= kWideMaxKeys &&
-           cu > 0 && groups >= cu && groups % cu == 0;
+           cu > 0 && groups == cu;
 }
 
 // BITCACHE_VALU_ATTENTION=1 selects the VALU split kernel for every head dim

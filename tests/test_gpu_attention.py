@@ -117,12 +117,11 @@ def test_many_groups_and_split_phase_api(F, shape):
     close(to_np(outpb).astype(np.float32), refb, what=f"split-phase binary {shape}")
     if shape == LAUNCH_SHAPES[0]:
         # 1536 MHA groups fill a round with one split each, in both plans: the
-        # full compensated call writes the output from the split kernel (no
-        # merge launch), bit for bit what the merge of the single partial
-        # gives.  (The full binary call runs one 8-wave workgroup per head when
-        # the heads fill the CUs in whole rounds, which sums in another order:
-        # checked against the oracle above.)
-        assert torch.equal(out, outp)
+        # full call writes the output from the split kernel (no merge launch),
+        # bit for bit what the merge of the single partial gives.  (Binary
+        # attention with exactly one head per CU runs one 8-wave workgroup per
+        # head instead; test_config_c2_full_size covers it.)
+        assert torch.equal(out, outp) and torch.equal(outb, outpb)
 
 
 def make_rising(B, Hq, Hkv, S, d, seed):
