@@ -208,18 +208,19 @@ def test_append_attend_in_a_hip_graph():
         assert torch.equal(cache._k_res, want_k), f"replay {rep}: cache bytes"
 
 
-@pytest.mark.parametrize("max_seq", [3000, 3001])
-def test_bitcache_attend_adaptive_partly_filled(max_seq):
-    """BitCache.attend_adaptive on a partly filled GQA ring (2000 of max_seq
+@pytest.mark.parametrize("max_seq,S", [(3000, 2000), (3001, 2000), (3000, 1999)])
+def test_bitcache_attend_adaptive_partly_filled(max_seq, S):
+    """BitCache.attend_adaptive on a partly filled GQA ring (S of max_seq
     tokens): the selection passes and the attention read rows at the ring's
-    stride; max_seq 3000 takes the eight-key scale loads, 3001 (stride not a
-    multiple of 8) the per-key ones.  Sets bit-exact, outputs against the
-    oracle (online encode of each group's tokens)."""
+    stride; max_seq 3000 takes the eight-key scale loads (with S = 1999 the
+    last eight-key run of each row ends past the row's tokens), 3001 (stride
+    not a multiple of 8) the per-key ones.  Sets bit-exact, outputs against
+    the oracle (online encode of each group's tokens)."""
     from bitcache_amd import BitCache
-    say(f"case bitcache adaptive partly filled max_seq={max_seq}")
-    B, Hq, Hkv, d, S, top_k = 2, 8, 2, 128, 2000, 200
+    say(f"case bitcache adaptive partly filled max_seq={max_seq} S={S}")
+    B, Hq, Hkv, d, top_k = 2, 8, 2, 128, 200
     G = Hq // Hkv
-    rng = np.random.default_rng(max_seq)
+    rng = np.random.default_rng(max_seq + S)
     k = (rng.standard_normal((B, Hkv, S, d)) * 0.2).astype(np.float16)
     v = (rng.standard_normal((B, Hkv, S, d)) * 0.2).astype(np.float16)
     q = (rng.standard_normal((B, Hq, d)) * 0.3).astype(np.float16)
