@@ -1660,15 +1660,10 @@ void attn_mfma_kernel(AttnArgs a) {
 
 // Wide workgroups (one split per group, the output written directly): MHA
 // binary attention at d = 128 with 8 waves; false for any other request.
-template <int D, int G>
-bool launch_wide(int mode, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
-    if constexpr (G == 1 && D == 128) {
-        if (mode == MODE_BINARY && nw == 8) {
-            hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a);
-            return true;
-        }
-    }
-    return false;
+bool launch_wide(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
+    if (mode != MODE_BINARY || D != 128 || G != 1 || nw != 8) return false;
+    hipLaunchKernelGGL((attn_mfma_kernel<128, 1, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a);
+    return true;
 }
 
 template <int D, int G>
@@ -1681,11 +1676,6 @@ void launch_dg(int mode, const AttnArgs& a, dim3 grid, hipStream_t st) {
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_MIXED>), grid, dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((attn_mfma_kernel<D, G, MODE_ADAPTIVE>), grid, dim3(256), 0, st, a);
-}
-
-template <int D>
-bool launch_wide_d(int mode, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
-    return G == 1 && launch_wide<D, 1>(mode, a, grid, st, nw);
 }
 
 template <int D>
@@ -1760,7 +1750,7 @@ bool launch_mfma_split(int mode, int D, int G, const AttnArgs& a, dim3 grid, hip
     if (!mfma_split_ok(D, a.chunk)) return false;
     // adaptive mode reads the popcounts stored by the selection passes
     if (mode == MODE_ADAPTIVE && a.pcs == nullptr) return false;
-    if (nw != 4) return D == 128 && launch_wide_d<128>(mode, G, a, grid, st, nw);
+    if (nw != 4) return launch_wide(mode, D, G, a, grid, st, nw);
     switch (D) {
         case 64: launch_d<64>(mode, G, a, grid, st); return true;
         case 128: launch_d<128>(mode, G, a, grid, st); return true;
