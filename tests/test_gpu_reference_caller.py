@@ -7,11 +7,12 @@ passes its binary buffer as the residual buffer, :104-111), and attends by
 handing *prefix views* ``buf[: batch*n_heads*filled*sizeof]`` to
 ``compensated_attention`` / ``binary_attention`` (:131-148).
 ``ReferenceCaller`` below restates that pattern in this test's own code and
-runs it against ``bitcache_amd._C`` -- the binding INTEGRATION.md tells a
-maintainer to add -- at B*H = 1 partly filled, B*H > 1 partly filled, and a
-full ring that has wrapped.  Outputs are checked against the oracle's
-attention over the tokens the ring holds (online-encode math, read with the
-ring's own stride), at the north_star tolerance; the reference's own
+runs it against ``bitcache_amd._C`` -- the operator module a caller of the
+reference imports in place of ``bitcache._C`` -- at B*H = 1 partly filled,
+B*H > 1 partly filled, and a full ring that has wrapped.  Outputs are checked
+against the oracle's attention over the tokens the ring holds (online-encode
+math, read with the ring's own stride), within 2e-3 max-abs relative error
+and cosine >= 0.9999; the reference's own
 checkpoints of tests/test_python.py:75-158 are replayed with their cosine
 bars against exact fp32 attention.
 """
