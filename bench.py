@@ -1,6 +1,6 @@
 """Benchmark: compensated decode attention over the compressed KV cache on one MI355X.
 
-Workload (BASELINE config c3): batch 8, 32 heads (MHA), head_dim 128, 64K
+Workload (config c3 of bitcache_amd/workloads.py): batch 8, 32 heads (MHA), head_dim 128, 64K
 context, one query token per sequence, Q/K/V ~ N(0, 1/128) with a per-token
 LogNormal(0, 0.25) factor on K and V, seed 2, cache pre-encoded (sign bits +
 fp16 scale + INT4 residual + fp16 scale) and resident in HBM.  A step is one

@@ -510,7 +510,7 @@ def topk_select(key: np.ndarray, k: int) -> np.ndarray:
 
 def adaptive_attention(Q, Kb, Kr, Vb, Vr, batch, n_heads, seq_len, top_k,
                        n_kv_heads=None, return_f32=False, return_sets=False):
-    """Adaptive precision (not in the reference, whose intent is
+    """Adaptive precision (config c5 of bitcache_amd/workloads.py; not in the reference, whose intent is
     src/adaptive_precision.cuh:6-12,33-41):  per (b, query head) select the top_k
     keys by topk_key; selected keys use the compensated score and V (binary +
     residual), the rest use the binary score and binary V; one softmax over all S."""

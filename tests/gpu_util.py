@@ -9,7 +9,7 @@ import torch
 
 from oracle import oracle as O
 
-# north_star tolerance for fp16/fp32 outputs: max-abs error relative to the
+# parity bar for fp16/fp32 outputs: max-abs error relative to the
 # largest reference magnitude <= 2e-3 and cosine similarity >= 0.9999.
 REL_TOL = 2e-3
 COS_TOL = 0.9999

@@ -178,7 +178,7 @@ def test_workspace_covers_every_split_plan(lib):
     partials of the plan every attention mode launches, on devices of several
     CU counts (the plan depends on the CU count), over shapes where the
     policies' split counts differ: MHA and GQA groups 1-8, short and long
-    contexts, the BASELINE shapes among them.  No launch: the plan is host
+    contexts, the c1-c5 config shapes among them.  No launch: the plan is host
     arithmetic.  (On a host without a GPU each mode plans at its largest
     workgroups-per-CU policy, the case with the most splits.)"""
     size_t = ctypes.c_size_t

@@ -1,5 +1,5 @@
 """Queries far from the Gaussian draws of the other tests, against the
-oracle at the north_star tolerance: a few channels scaled x10 and x100 (the
+oracle within 2e-3 max-abs relative error and cosine 0.9999: a few channels scaled x10 and x100 (the
 massive-activation channels of real decoder queries), fp16 extremes near
 65504, fp16 subnormals, and signed zeros.
 
