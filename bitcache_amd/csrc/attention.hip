@@ -963,12 +963,14 @@ int plan_per_cu(int mode, int D, int G) {
 // reference kernel
 constexpr int kPlanFixed = 0;
 
-// Binary MHA attention at d = 128 with one head per CU: one workgroup of
-// kWideWaves waves per head takes all its keys (wave w the tiles w, w + 8,
-// ...), merges its waves and writes the output, so the call writes no
-// partials and launches no merge.  Measured on the 256-head, 32K-key binary
-// step: 52.8-56.0 -> 47.0-48.1 us (the 4-wave plan: two workgroups per CU and
-// the merge launch); 16-wave workgroups 50.4-51.0 us.  With two or more heads
+// Binary MHA attention (d = 64, 128, 256: the matrix-core head dims) with one
+// head per CU: one workgroup of kWideWaves waves per head takes all its keys
+// (wave w the tiles w, w + 8, ...), merges its waves and writes the output,
+// so the call writes no partials and launches no merge.  Measured on the
+// 256-head, 32K-key binary step: d = 128 52.8-56.0 -> 47.0-48.1 us (the 4-wave
+// plan: two workgroups per CU and the merge launch; 16-wave workgroups
+// 50.4-51.0 us), d = 256 101.2-103.2 -> 96.8-97.3 us, d = 64 42.6-46.4 ->
+// 42.4-43.0 us.  With two or more heads
 // per CU the split plans already launch no merge and the wide plan measured
 // within noise of them (-4% to +2%), so it is left to one round.  Contexts up
 // to kWideMaxKeys (each wave's sums cover at most 16K keys, as in the split
@@ -983,8 +985,8 @@ bool wide_plan(int mode, int D, int G, int64_t groups, int S, int cu) {
         const char* e = getenv("BITCACHE_WIDE");
         return e != nullptr && atoi(e) == 0;
     }();
-    return !off && mode == MODE_BINARY && G == 1 && D == 128 && S > 0 && S <= kWideMaxKeys &&
-           cu > 0 && groups == cu;
+    return !off && mode == MODE_BINARY && G == 1 && (D == 64 || D == 128 || D == 256) && S > 0 &&
+           S <= kWideMaxKeys && cu > 0 && groups == cu;
 }
 
 // BITCACHE_VALU_ATTENTION=1 selects the VALU split kernel for every head dim

@@ -1659,11 +1659,16 @@ void attn_mfma_kernel(AttnArgs a) {
 }
 
 // Wide workgroups (one split per group, the output written directly): MHA
-// binary attention at d = 128 with 8 waves; false for any other request.
+// binary attention at d = 64, 128, 256 with 8 waves; false for any other
+// request.
 bool launch_wide(int mode, int D, int G, const AttnArgs& a, dim3 grid, hipStream_t st, int nw) {
-    if (mode != MODE_BINARY || D != 128 || G != 1 || nw != 8) return false;
-    hipLaunchKernelGGL((attn_mfma_kernel<128, 1, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a);
-    return true;
+    if (mode != MODE_BINARY || G != 1 || nw != 8) return false;
+    switch (D) {
+        case 64: hipLaunchKernelGGL((attn_mfma_kernel<64, 1, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a); return true;
+        case 128: hipLaunchKernelGGL((attn_mfma_kernel<128, 1, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a); return true;
+        case 256: hipLaunchKernelGGL((attn_mfma_kernel<256, 1, MODE_BINARY, 8>), grid, dim3(8 * 64), 0, st, a); return true;
+        default: return false;
+    }
 }
 
 template <int D, int G>

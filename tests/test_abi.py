@@ -214,10 +214,11 @@ def test_workspace_covers_every_split_plan(lib):
 
 
 def test_wide_binary_plan(lib):
-    """Binary MHA attention at d = 128 with one head per CU (and a context of
-    at most 131072 keys) plans one split per head: one wide workgroup takes all
-    of a head's keys and writes the output.  Other modes, GQA groups, other
-    head dims, longer contexts and other head counts keep the split plans."""
+    """Binary MHA attention at d = 64, 128, 256 with one head per CU (and a
+    context of at most 131072 keys) plans one split per head: one wide
+    workgroup takes all of a head's keys and writes the output.  Other modes,
+    GQA groups, the head dims without the matrix-core kernel, longer contexts
+    and other head counts keep the split plans."""
     size_t = ctypes.c_size_t
     f = lib.bc_attention_split_plan
     f.argtypes = [ctypes.c_int] * 7 + [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(size_t),
@@ -235,7 +236,9 @@ def test_wide_binary_plan(lib):
     assert splits(0, 8, 32, 32, 32768, 128, 80) > 1          # 256 heads on 80 CUs
     assert splits(0, 8, 32, 32, 32768, 128, 512) > 1         # half a round
     assert splits(0, 4, 32, 32, 131136, 128, 128) > 1        # past the wide context
-    assert splits(0, 8, 32, 32, 32768, 64, 256) > 1          # another head dim
+    assert splits(0, 8, 32, 32, 32768, 64, 256) == 1         # d = 64
+    assert splits(0, 8, 32, 32, 32768, 256, 256) == 1        # d = 256
+    assert splits(0, 8, 32, 32, 32768, 96, 256) > 1          # a VALU-kernel head dim
     assert splits(0, 8, 32, 8, 32768, 128, 64) > 1           # GQA groups
     assert splits(1, 8, 32, 32, 32768, 128, 256) > 1         # compensated
     assert splits(3, 8, 32, 32, 32768, 128, 256) > 1         # per-head modes

@@ -370,28 +370,29 @@ def test_config_c2_full_size_scores(F):
     assert cosh.min() >= 0.9999
 
 
-def test_wide_binary_longest_context(F):
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_wide_binary_longest_context(F, d):
     """Binary MHA attention with one head per CU runs one 8-wave workgroup per
-    head (no split partials, no merge launch); at the longest context that
-    plan takes (131072 keys: 16384 keys, 256 tiles, per wave) 16 heads spread
-    over the batch agree with the torch-CPU restatement of the reference's
-    binary attention (src/binary_attention.cu:8-82).  Keys equal to 2q sit at
-    200 positions of the last quarter, so each wave's running softmax
-    reference moves after thousands of keys and those keys carry most of the
-    weight."""
+    head (no split partials, no merge launch) at every matrix-core head dim;
+    at the longest context that plan takes (131072 keys: 16384 keys, 256
+    tiles, per wave) 16 heads spread over the batch agree with the torch-CPU
+    restatement of the reference's binary attention
+    (src/binary_attention.cu:8-82).  Keys equal to 2q sit at 200 positions of
+    the last quarter, so each wave's running softmax reference moves after
+    thousands of keys and those keys carry most of the weight."""
     import ctypes
     import os
     cu = torch.cuda.get_device_properties(0).multi_processor_count
     if cu % 32:
         pytest.skip(f"{cu} CUs: no batch of 32-head sequences gives one head per CU")
-    B, H, S, d = cu // 32, 32, 131072, 128
+    B, H, S = cu // 32, 32, 131072
     lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
                                    "bitcache_amd", "libbitcache_hip.so"))
     ns, pb, wb = ctypes.c_int(0), ctypes.c_size_t(0), ctypes.c_size_t(0)
     assert lib.bc_attention_split_plan(0, B, H, H, S, d, 0, ctypes.byref(ns), ctypes.byref(pb),
                                        ctypes.byref(wb)) == 0
     assert ns.value == 1, "binary MHA with one head per CU plans one wide workgroup per head"
-    say(f"case wide binary B={B} H={H} S={S}")
+    say(f"case wide binary B={B} H={H} S={S} d={d}")
     g = torch.Generator(device="cuda")
     g.manual_seed(131)
     q = (torch.randn((B, H, d), generator=g, device="cuda") * 0.1).half()
@@ -415,7 +416,7 @@ def test_wide_binary_longest_context(F):
         kw, ks = bin_head_tensors(kb, n, d, (b * H + h) * S, S)
         vw, vs = bin_head_tensors(vb, n, d, (b * H + h) * S, S)
         ref[i] = O.binary_attention_torch_cpu(qc[b, h][None], kw, ks, vw, vs)[0].float().numpy()
-    close(got, ref, what="wide binary attention, 131072 keys")
+    close(got, ref, what=f"wide binary attention, 131072 keys, d = {d}")
 
 
 def test_fp32_order_kats(F):
