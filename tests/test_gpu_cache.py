@@ -208,6 +208,32 @@ def test_append_attend_in_a_hip_graph():
         assert torch.equal(cache._k_res, want_k), f"replay {rep}: cache bytes"
 
 
+def test_bitcache_binary_ring_one_head_per_cu():
+    """A binary-mode BitCache with one head per CU (the one-workgroup-per-head
+    plan) on a partly filled ring (2001 of 3000 tokens): the attention reads
+    each head's row at the ring's stride and stops at its last token; eight
+    heads against the oracle's binary attention over those tokens (online
+    encode)."""
+    from bitcache_amd import BitCache
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    if cu % 32:
+        pytest.skip(f"{cu} CUs: no batch of 32-head sequences gives one head per CU")
+    B, H, d, max_seq, S = cu // 32, 32, 128, 3000, 2001
+    say(f"case bitcache binary ring B={B} H={H} S={S} max_seq={max_seq}")
+    rng = np.random.default_rng(2001)
+    k = (rng.standard_normal((B, H, S, d)) * 0.2).astype(np.float16)
+    v = (rng.standard_normal((B, H, S, d)) * 0.2).astype(np.float16)
+    q = (rng.standard_normal((B, H, d)) * 0.3).astype(np.float16)
+    cache = BitCache(B, H, d, max_seq, compensated=False)
+    cache.prefill(torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    out = to_np(cache.attend(torch.from_numpy(q).cuda())).astype(np.float32)
+    for (b, h) in [(0, 0), (0, 31), (1, 7), (2, 15), (3, 3), (B - 1, 0), (B - 1, 16), (B // 2, 30)]:
+        Kb, _ = O.online_encode(k[b, h])
+        Vb, _ = O.online_encode(v[b, h])
+        _, ref = O.binary_attention(q[b, h][None, None], Kb, Vb, 1, 1, S, return_f32=True)
+        close(out[b, h][None], ref[0], what=f"binary ring head {(b, h)}")
+
+
 @pytest.mark.parametrize("max_seq,S", [(3000, 2000), (3001, 2000), (3000, 1999)])
 def test_bitcache_attend_adaptive_partly_filled(max_seq, S):
     """BitCache.attend_adaptive on a partly filled GQA ring (S of max_seq
