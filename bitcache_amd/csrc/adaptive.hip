@@ -478,7 +478,12 @@ __global__ __launch_bounds__(256) void collect_kernel(SelArgs a) {
                         for (int g = 0; g < G; g++) {
                             const float sc = fmaf((float)pc_of(st, u, j, g), sk2, nd);
                             const bool in = sc > flo_f[g] && sc <= fhi[g];
-                            const uint64_t m = __ballot(in);
+                            // the same test as the two compares' lane masks
+                            // ANDed (a ballot of `in` would first copy the
+                            // flag through a vector register: two more VALU
+                            // instructions per key and head)
+                            const uint64_t m = __builtin_amdgcn_fcmpf(sc, flo_f[g], 2 /* ordered > */) &
+                                               __builtin_amdgcn_fcmpf(sc, fhi[g], 5 /* ordered <= */);
                             if (m != 0ull) {
                                 if (in) {
                                     const uint32_t below = __builtin_amdgcn_mbcnt_hi(
